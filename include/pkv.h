@@ -1,0 +1,165 @@
+/*
+ * pkv.h -- C ABI of libpkv, the MI355X (gfx950) paged-KV decode path.
+ *
+ * The reference (SSusantAchary/mlx-one) has no FFI on this path: its hot path
+ * is Python calling MLX ops and one generated Metal kernel.  Each entry point
+ * below replaces the reference code named in its comment; the Python host
+ * package (mlx-one_amd/pkv) binds them with ctypes behind the reference's own
+ * class and function names.
+ *
+ * Conventions
+ *  - All pointers except `layout` are device pointers (HBM) unless noted; sizes
+ *    are element counts.  No entry point allocates device memory: the caller
+ *    owns every buffer, including the attention workspace.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).  Work
+ *    is enqueued asynchronously; entry points never synchronise.
+ *  - Return value: PKV_OK or an error code; pkv_last_error() gives the text of
+ *    the calling thread's last error.
+ *  - Entry points are re-entrant; calls on different streams may overlap as
+ *    long as they do not write the same pages or workspace.
+ */
+#ifndef PKV_H
+#define PKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum pkv_status {
+  PKV_OK = 0,
+  PKV_INVALID_ARGUMENT = 1, /* shape, layout or mapping errors (reference: ValueError) */
+  PKV_UNSUPPORTED = 2,      /* reference: ModelCapabilityUnsupported */
+  PKV_OUT_OF_MEMORY = 3,    /* workspace too small (reference: CacheCapacityError) */
+  PKV_LAUNCH_FAILED = 4     /* HIP runtime error */
+};
+
+/*
+ * Page layout of one layer's pool.  Mirrors the reference's BlockLayout
+ * (src/mlx_one/engine/block_cache.py:32-43): num_kv_heads, head_dim,
+ * page_tokens, quantization_bits (16 = unquantized), quantization_group_size.
+ * float_kind selects the float element type of unquantized pages, queries,
+ * new K/V and outputs: 0 = bfloat16, 1 = float16 (key_dtype/value_dtype).
+ */
+typedef struct pkv_layout {
+  int32_t num_kv_heads;
+  int32_t head_dim;     /* 1..256 */
+  int32_t page_tokens;  /* 16, 32, 64 or 128 */
+  int32_t bits;         /* 4, 8 (affine quantized) or 16 (float pages) */
+  int32_t group_size;   /* 32, 64 or 128 for quantized pages */
+  int32_t float_kind;   /* 0 = bf16, 1 = f16 */
+} pkv_layout;
+
+/* Library version (increments when the page format or an ABI changes). */
+int pkv_version(void);
+
+/* Thread-local text of the last error; never NULL. */
+const char *pkv_last_error(void);
+
+/* Bytes of one page (all KV heads) in the pool; <0 when the layout is invalid.
+ * Replaces the per-segment tensor shapes of SegmentedPageArena
+ * (src/mlx_one/engine/arena.py:58-75). */
+int64_t pkv_page_bytes(const pkv_layout *layout);
+
+/* Head dimension as stored (padded to 64, 128 or 256); <0 when invalid. */
+int32_t pkv_stored_dim(const pkv_layout *layout);
+
+/*
+ * Append `tokens` new K/V tokens per sequence into their pages, quantizing each
+ * (head, token) group-wise as it is written (affine unsigned, f16 scale and
+ * bias, the reference's quantize_page arithmetic).
+ * Replaces PagedKVCache.append + quantize_page
+ * (src/mlx_one/engine/paged.py:103-154 and :24-41) and the arena staging it
+ * triggers (src/mlx_one/engine/arena.py:90-113).
+ *
+ *  keys, values : [batch][num_kv_heads][tokens][head_dim], float_kind elements
+ *  block_table  : [batch][max_pages] int32 page ids (pages must already be
+ *                 assigned for every position written)
+ *  start_pos    : [batch] int32 length of each sequence before the append
+ *  widths       : [batch] int32 tokens to append per sequence (<= tokens), or
+ *                 NULL for `tokens` everywhere
+ *  new_lens     : [batch] int32 output start_pos + width, or NULL
+ */
+int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int64_t num_pages,
+                        const void *keys, const void *values, int32_t batch, int32_t tokens,
+                        const int32_t *block_table, int32_t max_pages,
+                        const int32_t *start_pos, const int32_t *widths, int32_t *new_lens);
+
+/*
+ * Causal GQA paged attention for decode (num_queries = 1) and speculative
+ * verify (num_queries = 1 + drafts): dequantization fused into the page load,
+ * split-K over token partitions of `split_tokens`, log-sum-exp merge.
+ * Replaces paged_attention and its Metal kernel
+ * (src/mlx_one/engine/paged_attention.py:62-124 kernel, :127-206 dispatch and
+ * partition merge).
+ *
+ *  queries      : [batch][num_heads][num_queries][head_dim], float_kind
+ *  seq_lens     : [batch] tokens in each sequence's cache (after the append)
+ *  q_pos        : [batch][num_queries] logical query positions, or NULL for
+ *                 seq_lens[b] - widths[b] + q; token t is visible to query q
+ *                 when t <= q_pos (paged_attention.py:81)
+ *  widths       : [batch] real query rows (rows q >= widths[b] output 0), or NULL
+ *  scale        : softmax scale
+ *  split_tokens : tokens per partition, a multiple of page_tokens, at most
+ *                 64 pages; 0 picks a default
+ *  max_units    : number of (sequence, partition) pairs to launch for, at least
+ *                 sum_b max(1, ceil(seq_lens[b] / split_tokens)); extra ones exit
+ *  workspace    : device scratch of pkv_attention_workspace_bytes(...) bytes
+ *  out          : [batch][num_heads][num_queries][head_dim], float_kind
+ */
+int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool,
+                        int64_t num_pages, const void *queries, int32_t batch,
+                        int32_t num_heads, int32_t num_queries, const int32_t *block_table,
+                        int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
+                        const int32_t *widths, float scale, int32_t split_tokens,
+                        int32_t max_units, void *workspace, int64_t workspace_bytes, void *out);
+
+/* Workspace bytes pkv_paged_attention needs for `max_units` partitions. */
+int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
+                                      int32_t num_queries, int32_t max_units);
+
+/*
+ * Copy pages out of the pool into the reference's per-page tensor format
+ * (paged_attention.py:31-35): quantized pages give K codes [count][HK][P][Dq]
+ * u8 (Dq = Dp for 8 bit, Dp/2 for 4 bit, Dp = ceil(D/G)*G), K scale and K bias
+ * [count][HK][P][Dp/G] f16, then the same for V; float pages give K and V
+ * [count][HK][P][D] (the three V-side / scale pointers are then unused and may
+ * be NULL).  Bit-exact copies: the block-table gather behind the reference's
+ * page views (arena.py:101-106) and dequantize_page's input (paged.py:44-54).
+ */
+int pkv_gather_pages(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
+                     const int32_t *page_ids, int32_t count, void *k_codes, void *k_scale,
+                     void *k_bias, void *v_codes, void *v_scale, void *v_bias);
+
+/*
+ * Copy whole pages src_ids[i] -> dst_ids[i] inside the pool (copy-on-write of a
+ * shared mutable tail page).  Replaces the tail copy in PagedKVCache.clone
+ * (src/mlx_one/engine/paged.py:83-91).
+ */
+int pkv_copy_pages(void *stream, const pkv_layout *layout, void *pool, int64_t num_pages,
+                   const int32_t *src_ids, const int32_t *dst_ids, int32_t count);
+
+/*
+ * Quantize `rows` rows of `dim` float_kind values into the reference's page
+ * tensors: codes [rows][Dq] u8, scale and bias [rows][Dp/G] f16 bits
+ * (Dp = ceil(dim/G)*G, Dq = Dp or Dp/2 for 4 bit; 4-bit packs
+ * code[2i] | code[2i+1] << 4).  Replaces quantize_page
+ * (src/mlx_one/engine/paged.py:24-41) with group_size as a parameter
+ * (the reference hard-codes 32).
+ */
+int pkv_quantize_rows(void *stream, const void *values, int64_t rows, int32_t dim, int32_t bits,
+                      int32_t group_size, int32_t float_kind, void *codes, void *scale, void *bias);
+
+/*
+ * x = f32(code) * f32(scale) + f32(bias), float32 out [rows][dim].  Replaces
+ * dequantize_page (src/mlx_one/engine/paged.py:44-54).
+ */
+int pkv_dequantize_rows(void *stream, const void *codes, const void *scale, const void *bias,
+                        int64_t rows, int32_t dim, int32_t bits, int32_t group_size, void *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKV_H */

@@ -1,0 +1,247 @@
+"""Functional layer over libpkv: torch device tensors in and out.
+
+These are the primitives the reference-named classes (``pkv.arena``,
+``pkv.paged``, ``pkv.paged_attention``) are built on.  Every function enqueues
+HIP work on the current torch stream through the C ABI and never falls back to
+a CPU implementation.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from pkv import _native as nat
+
+FLOAT_KINDS = {torch.bfloat16: 0, torch.float16: 1}
+DTYPES = {0: torch.bfloat16, 1: torch.float16}
+DEFAULT_SPLIT_TOKENS = 256
+
+
+@dataclass(frozen=True)
+class PageFormat:
+    """One layer's page layout; the C ``pkv_layout`` plus derived sizes.
+
+    ``bits`` is 4 or 8 for affine-quantized pages and 16 for float pages
+    (the reference's ``BlockLayout.quantization_bits`` None).
+    """
+
+    num_kv_heads: int
+    head_dim: int
+    page_tokens: int
+    bits: int = 16
+    group_size: int = 32
+    dtype: torch.dtype = torch.bfloat16
+
+    def __post_init__(self):
+        if self.dtype not in FLOAT_KINDS:
+            from pkv.modes import ModelCapabilityUnsupported
+
+            raise ModelCapabilityUnsupported("unsupported paged storage precision")
+        if self.page_bytes < 0:
+            nat.check(nat.PKV_UNSUPPORTED, "page layout")
+
+    @property
+    def c_layout(self):
+        return nat.Layout(self.num_kv_heads, self.head_dim, self.page_tokens, self.bits,
+                          self.group_size if self.bits != 16 else 32, FLOAT_KINDS[self.dtype])
+
+    @property
+    def page_bytes(self):
+        return int(nat.load().pkv_page_bytes(self.c_layout))
+
+    @property
+    def stored_dim(self):
+        return int(nat.load().pkv_stored_dim(self.c_layout))
+
+    @property
+    def quantized(self):
+        return self.bits != 16
+
+    @property
+    def reference_dim(self):
+        """Padded head dim of the reference format (``paged.py:31``)."""
+        if not self.quantized:
+            return self.head_dim
+        return (self.head_dim + self.group_size - 1) // self.group_size * self.group_size
+
+
+def allocate_pool(fmt: PageFormat, num_pages: int, device="cuda"):
+    """Device page pool ``[num_pages, page_bytes]`` uint8 (zeroed)."""
+    return torch.zeros((num_pages, fmt.page_bytes), dtype=torch.uint8, device=device)
+
+
+def _i32(x, device):
+    if x is None:
+        return None
+    if isinstance(x, torch.Tensor):
+        t = x.to(device=device, dtype=torch.int32)
+    else:
+        t = torch.as_tensor(x, dtype=torch.int32).to(device)
+    return t.contiguous()
+
+
+def _check_float(t, fmt, name):
+    if t.dtype != fmt.dtype:
+        raise ValueError(f"{name} dtype {t.dtype} differs from the page dtype {fmt.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+
+
+def append_quantize(fmt: PageFormat, pool, keys, values, block_table, start_pos, widths=None,
+                    new_lens=None):
+    """Write ``keys/values [B, HK, T, D]`` at positions ``start_pos[b] + t``."""
+    if keys.shape != values.shape or keys.dim() != 4:
+        raise ValueError("paged append requires matching [B, HK, T, D] K/V tensors")
+    batch, heads, tokens, dim = keys.shape
+    if heads != fmt.num_kv_heads or dim != fmt.head_dim:
+        raise ValueError("paged append layout mismatch")
+    _check_float(keys, fmt, "keys")
+    _check_float(values, fmt, "values")
+    device = keys.device
+    table = _i32(block_table, device)
+    if table.dim() != 2 or table.shape[0] != batch:
+        raise ValueError("block table must be [batch, max_pages]")
+    start = _i32(start_pos, device)
+    width = _i32(widths, device)
+    keys, values = keys.contiguous(), values.contiguous()
+    code = nat.load().pkv_append_quantize(
+        nat.stream_handle(device), fmt.c_layout, nat.ptr(pool), pool.shape[0], nat.ptr(keys),
+        nat.ptr(values), batch, tokens, nat.ptr(table), table.shape[1], nat.ptr(start),
+        nat.ptr(width), nat.ptr(new_lens))
+    nat.check(code, "paged append")
+
+
+def plan_partitions(lengths, page_tokens, num_kv_heads=1, split_tokens=0, target_waves=4096):
+    """Partition size and unit count for host-known sequence lengths.
+
+    One wave of the attention kernel handles one (sequence, partition, KV
+    head).  ``split_tokens`` (a multiple of the page, 128..1024 tokens) is
+    chosen so that the launch has about ``target_waves`` waves -- enough to
+    keep every CU of the chip streaming -- and ``(split_tokens, units)`` is
+    returned with ``units = sum_b max(1, ceil(L_b / split))``.
+    """
+    lengths = [int(x) for x in lengths]
+    if split_tokens <= 0:
+        total = sum(max(x, 1) for x in lengths)
+        target_units = max(1, target_waves // max(num_kv_heads, 1))
+        split = max(DEFAULT_SPLIT_TOKENS // 2, min(1024, total // target_units))
+        split = max(page_tokens, (split + page_tokens - 1) // page_tokens * page_tokens)
+        split = min(split, 64 * page_tokens)
+        split_tokens = split
+    units = sum(max(1, math.ceil(x / split_tokens)) for x in lengths)
+    return split_tokens, units
+
+
+def workspace_bytes(fmt: PageFormat, num_heads, num_queries, units):
+    return int(nat.load().pkv_attention_workspace_bytes(fmt.c_layout, num_heads, num_queries,
+                                                          units))
+
+
+def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, scale, q_pos=None,
+                    widths=None, split_tokens=0, units=None, lengths_host=None, workspace=None,
+                    out=None):
+    """Attention of ``queries [B, H, Q, D]`` over the paged cache.
+
+    ``seq_lens`` counts the tokens in each sequence's cache (after the
+    append).  ``units`` / ``split_tokens`` may be given; otherwise they come
+    from ``lengths_host`` (host ints) or a copy of ``seq_lens`` to the host.
+    """
+    if queries.dim() != 4:
+        raise ValueError("queries must be [B, H, Q, D]")
+    batch, heads, nq, dim = queries.shape
+    if dim != fmt.head_dim:
+        raise ValueError("query head dimension differs from the page layout")
+    _check_float(queries, fmt, "queries")
+    device = queries.device
+    table = _i32(block_table, device)
+    lens = _i32(seq_lens, device)
+    if units is None or split_tokens <= 0:
+        host = lengths_host if lengths_host is not None else lens.cpu().tolist()
+        split_tokens, units = plan_partitions(host, fmt.page_tokens, fmt.num_kv_heads,
+                                              split_tokens)
+    need = workspace_bytes(fmt, heads, nq, units)
+    if units > batch and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if out is None:
+        out = torch.empty_like(queries)
+    queries = queries.contiguous()
+    code = nat.load().pkv_paged_attention(
+        nat.stream_handle(device), fmt.c_layout, nat.ptr(pool), pool.shape[0], nat.ptr(queries),
+        batch, heads, nq, nat.ptr(table), table.shape[1], nat.ptr(lens),
+        nat.ptr(_i32(q_pos, device)), nat.ptr(_i32(widths, device)), float(scale),
+        int(split_tokens), int(units), nat.ptr(workspace),
+        0 if workspace is None else workspace.numel(), nat.ptr(out))
+    nat.check(code, "paged attention")
+    return out
+
+
+def gather_pages(fmt: PageFormat, pool, page_ids):
+    """Pages in the reference's per-page tensor format (``paged_attention.py:31-35``).
+
+    Quantized: ``(k_codes [N,HK,P,Dq] u8, k_scale [N,HK,P,Dp/G] f16, k_bias,
+    v_codes, v_scale, v_bias)``; float: ``(k [N,HK,P,D], v)``.
+    """
+    ids = _i32(page_ids, pool.device)
+    n = ids.numel()
+    shape = (n, fmt.num_kv_heads, fmt.page_tokens)
+    if fmt.quantized:
+        dq = fmt.reference_dim * fmt.bits // 8
+        ng = fmt.reference_dim // fmt.group_size
+        kc = torch.empty(shape + (dq,), dtype=torch.uint8, device=pool.device)
+        vc = torch.empty_like(kc)
+        ks, kb, vs, vb = (torch.empty(shape + (ng,), dtype=torch.float16, device=pool.device)
+                          for _ in range(4))
+        outs = (kc, ks, kb, vc, vs, vb)
+    else:
+        k = torch.empty(shape + (fmt.head_dim,), dtype=fmt.dtype, device=pool.device)
+        v = torch.empty_like(k)
+        outs = (k, None, None, v, None, None)
+    code = nat.load().pkv_gather_pages(nat.stream_handle(pool.device), fmt.c_layout,
+                                       nat.ptr(pool), pool.shape[0], nat.ptr(ids), n,
+                                       *[nat.ptr(t) for t in outs])
+    nat.check(code, "page gather")
+    return outs if fmt.quantized else (outs[0], outs[3])
+
+
+def copy_pages(fmt: PageFormat, pool, src_ids, dst_ids):
+    src = _i32(src_ids, pool.device)
+    dst = _i32(dst_ids, pool.device)
+    if src.numel() != dst.numel():
+        raise ValueError("page copy requires matching id lists")
+    code = nat.load().pkv_copy_pages(nat.stream_handle(pool.device), fmt.c_layout, nat.ptr(pool),
+                                     pool.shape[0], nat.ptr(src), nat.ptr(dst), src.numel())
+    nat.check(code, "page copy")
+
+
+def quantize_rows(values, bits, group_size=32):
+    """Reference ``quantize_page`` over the last axis: ``(codes, scale f16, bias f16)``."""
+    if values.dtype not in FLOAT_KINDS:
+        raise ValueError("quantize expects float16 or bfloat16 values")
+    values = values.contiguous()
+    dim = values.shape[-1]
+    rows = values.numel() // dim if dim else 0
+    padded = (dim + group_size - 1) // group_size * group_size
+    lead = tuple(values.shape[:-1])
+    codes = torch.empty(lead + (padded * bits // 8,), dtype=torch.uint8, device=values.device)
+    scale = torch.empty(lead + (padded // group_size,), dtype=torch.float16, device=values.device)
+    bias = torch.empty_like(scale)
+    code = nat.load().pkv_quantize_rows(nat.stream_handle(values.device), nat.ptr(values), rows,
+                                        dim, bits, group_size, FLOAT_KINDS[values.dtype],
+                                        nat.ptr(codes), nat.ptr(scale), nat.ptr(bias))
+    nat.check(code, "quantize")
+    return codes, scale, bias
+
+
+def dequantize_rows(state, bits, dim, group_size=32):
+    """Reference ``dequantize_page``: float32 ``[..., dim]``."""
+    codes, scale, bias = (t.contiguous() for t in state)
+    rows = scale.numel() // scale.shape[-1] if scale.dim() else 0
+    out = torch.empty(tuple(codes.shape[:-1]) + (dim,), dtype=torch.float32, device=codes.device)
+    code = nat.load().pkv_dequantize_rows(nat.stream_handle(codes.device), nat.ptr(codes),
+                                          nat.ptr(scale), nat.ptr(bias), rows, dim, bits,
+                                          group_size, nat.ptr(out))
+    nat.check(code, "dequantize")
+    return out

@@ -1,0 +1,217 @@
+"""GPU parity: libpkv (through the C ABI) against the CPU oracle on seeded inputs.
+
+Bars (north star): bit-exact quantized codes, scales, biases and block-table
+gathers; attention within 2e-2 max-abs and 1e-3 mean-abs in bf16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import cport, numpy_ref
+from paged_case import (assert_attention_close, fill_pages, oracle_attention, oracle_pages,
+                        scale_of, to_torch)
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pkv import _native
+
+    _native.load()  # fails loudly when libpkv.so is missing
+
+
+def _fmt(w, dtype=None):
+    from pkv.ops import PageFormat
+
+    return PageFormat(w.kv_heads, w.head_dim, w.page_tokens, w.bits, w.group_size,
+                      dtype or torch.bfloat16)
+
+
+# ---------------------------------------------------------------- quantizer
+
+
+GOLDEN = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "quantize_page_g32.npz")
+CASES = sorted({k.split("/")[0] for k in GOLDEN.files})
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_rows_matches_reference_golden(case, bits):
+    from pkv import ops
+
+    x = GOLDEN[f"{case}/input"]
+    dtype = torch.float16 if x.dtype == np.float16 else torch.bfloat16
+    t = torch.from_numpy(x.astype(np.float32)).to("cuda", dtype)
+    codes, scale, bias = ops.quantize_rows(t, bits, 32)
+    torch.cuda.synchronize()
+    assert np.array_equal(codes.cpu().numpy(), GOLDEN[f"{case}/b{bits}/codes"])
+    assert np.array_equal(scale.cpu().numpy().view(np.uint16),
+                          GOLDEN[f"{case}/b{bits}/scale"].view(np.uint16))
+    assert np.array_equal(bias.cpu().numpy().view(np.uint16),
+                          GOLDEN[f"{case}/b{bits}/bias"].view(np.uint16))
+    restored = ops.dequantize_rows((codes, scale, bias), bits, x.shape[-1], 32)
+    assert np.array_equal(restored.cpu().numpy(), GOLDEN[f"{case}/b{bits}/dequant"])
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_quantize_rows_matches_c_oracle(group, bits, dtype):
+    from pkv import ops
+
+    rng = np.random.default_rng(7 + group + bits)
+    x = rng.standard_normal((2048, 128)).astype(np.float32)
+    x[:, rng.choice(128, 2, replace=False)] *= 8
+    x[::97] *= 300.0           # wide groups
+    x[5::113] = 0.25           # constant groups
+    x = x.astype(np.float16).astype(np.float32) if dtype == "float16" else numpy_ref.bf16_round(x)
+    t = torch.from_numpy(x).to("cuda", getattr(torch, dtype))
+    codes, scale, bias = ops.quantize_rows(t, bits, group)
+    want = cport.quantize_rows(x, bits, group)
+    assert np.array_equal(codes.cpu().numpy(), want[0])
+    assert np.array_equal(scale.cpu().numpy().view(np.uint16), want[1].view(np.uint16))
+    assert np.array_equal(bias.cpu().numpy().view(np.uint16), want[2].view(np.uint16))
+
+
+# ------------------------------------------------------- append + gather
+
+
+LAYOUTS = [
+    # bits, head_dim, group, page, dtype, chunk
+    (8, 128, 64, 16, "bfloat16", 1),
+    (8, 128, 64, 16, "bfloat16", 37),
+    (8, 128, 32, 32, "float16", 5),
+    (8, 128, 128, 16, "bfloat16", 64),
+    (4, 128, 64, 32, "bfloat16", 7),
+    (4, 128, 32, 16, "float16", 16),
+    (8, 64, 32, 16, "bfloat16", 9),
+    (4, 64, 64, 64, "bfloat16", 33),
+    (8, 37, 32, 16, "float16", 11),
+    (4, 256, 64, 16, "bfloat16", 3),
+    (16, 64, 32, 16, "bfloat16", 13),
+    (16, 128, 32, 32, "float16", 5),
+    (16, 100, 32, 16, "bfloat16", 17),
+]
+
+
+def _small(bits, dim, group, page, batch=3, lengths=(1, 40, 77), seed=11):
+    from pkv import workloads
+
+    return workloads.Workload("t", batch=batch, heads=4 * 2, kv_heads=2, head_dim=dim,
+                              page_tokens=page, bits=bits, group_size=group,
+                              lengths=tuple(lengths), seed=seed)
+
+
+@pytest.mark.parametrize("bits,dim,group,page,dtype,chunk", LAYOUTS)
+def test_append_then_gather_is_bit_exact(bits, dim, group, page, dtype, chunk):
+    from pkv import ops, workloads
+
+    w = _small(bits, dim, group, page)
+    inst = workloads.generate(w)
+    if dtype == "float16":
+        inst.keys = [k.astype(np.float16).astype(np.float32) for k in inst.keys]
+        inst.values = [v.astype(np.float16).astype(np.float32) for v in inst.values]
+    fmt = _fmt(w, getattr(torch, dtype))
+    pool, table, lengths = fill_pages(fmt, inst, chunk=chunk)
+    ref = numpy_ref.RefPages(w.kv_heads, dim, page, bits=None if bits == 16 else bits,
+                             group_size=group, dtype=dtype, tail="quantized")
+    for b in range(w.batch):
+        ref.write_sequence(inst.table[b], inst.keys[b], inst.values[b])
+    ids = sorted(ref.pages)
+    raw = lambda t: (t.view(torch.int16).cpu().numpy().view(np.uint16) if t.element_size() == 2
+                     else t.cpu().numpy())
+    got = [raw(t) for t in ops.gather_pages(fmt, pool, ids)]
+    for i, pid in enumerate(ids):
+        count = ref.pages[pid][2]
+        for g_arr, w_arr in zip(got, ref.state(pid)):
+            w_page = np.asarray(w_arr)[:, :count]
+            if w_page.dtype == np.float16:
+                w_bits = w_page.view(np.uint16)
+            elif w_page.dtype == np.float32:   # float pages, values already in page dtype
+                w_bits = (w_page.astype(np.float16).view(np.uint16) if dtype == "float16" else
+                          (w_page.view(np.uint32) >> 16).astype(np.uint16))
+            else:
+                w_bits = w_page
+            assert np.array_equal(g_arr[i][:, :count], w_bits), f"page {pid}"
+
+
+def test_copy_pages_duplicates_page_bytes():
+    from pkv import ops
+
+    w = _small(8, 128, 64, 16)
+    fmt = _fmt(w)
+    pool = torch.randint(0, 256, (8, fmt.page_bytes), dtype=torch.uint8, device="cuda")
+    ops.copy_pages(fmt, pool, [1, 3], [6, 7])
+    torch.cuda.synchronize()
+    assert torch.equal(pool[6], pool[1]) and torch.equal(pool[7], pool[3])
+
+
+# ------------------------------------------------------------- attention
+
+
+ATTN_CASES = {
+    # name: (workload overrides, dtype, chunk, split_tokens)
+    "c1_bf16": (dict(name="c1"), "bfloat16", 64, 0),
+    "c1_bf16_split": (dict(name="c1"), "bfloat16", 128, 64),
+    "c2_small": (dict(name="c2", batch=4, length_range=(1, 900)), "bfloat16", 100, 0),
+    "c2_small_split": (dict(name="c2", batch=5, length_range=(17, 700)), "bfloat16", 50, 128),
+    "c2_g32_f16": (dict(name="c2", batch=3, length_range=(100, 400), group_size=32), "float16", 64, 64),
+    "c3_small": (dict(name="c3", batch=2, lengths=(1500, 2048)), "bfloat16", 512, 512),
+    "c4_small": (dict(name="c4", batch=4, length_range=(300, 700)), "bfloat16", 128, 0),
+    "c4_split": (dict(name="c4", batch=3, length_range=(260, 520)), "bfloat16", 64, 64),
+    "d37_int8": (dict(name="c2", batch=3, length_range=(20, 200), head_dim=37, group_size=32),
+                 "bfloat16", 40, 32),
+    "f16_pages": (dict(name="c1", bits=16), "float16", 64, 32),
+}
+
+
+@pytest.mark.parametrize("case", sorted(ATTN_CASES))
+def test_attention_matches_oracle(case):
+    from pkv import ops, workloads
+
+    overrides, dtype, chunk, split = ATTN_CASES[case]
+    overrides = dict(overrides)
+    w = workloads.get(overrides.pop("name"), **overrides)
+    inst = workloads.generate(w)
+    if dtype == "float16":
+        inst.keys = [k.astype(np.float16).astype(np.float32) for k in inst.keys]
+        inst.values = [v.astype(np.float16).astype(np.float32) for v in inst.values]
+        inst.queries = inst.queries.astype(np.float16).astype(np.float32)
+    fmt = _fmt(w, getattr(torch, dtype))
+    pool, table, lengths = fill_pages(fmt, inst, chunk=chunk)
+    positions = inst.positions
+    widths = np.full(w.batch, w.num_queries, np.int32)
+    scale = scale_of(w.head_dim)
+    q = to_torch(inst.queries, fmt.dtype)
+    out = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale,
+                              q_pos=torch.from_numpy(positions).cuda(), split_tokens=split)
+    torch.cuda.synchronize()
+    want = oracle_attention(fmt, inst, positions, widths, scale)
+    assert_attention_close(out.float().cpu().numpy(), want)
+
+
+def test_attention_padded_query_rows_are_zero():
+    from pkv import ops, workloads
+
+    w = workloads.get("c4", batch=3, length_range=(200, 300))
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    widths = np.array([5, 2, 1], np.int32)
+    positions = inst.positions
+    scale = scale_of(w.head_dim)
+    out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
+                              scale=scale, q_pos=torch.from_numpy(positions).cuda(),
+                              widths=torch.from_numpy(widths).cuda(), split_tokens=64)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = oracle_attention(fmt, inst, positions, widths, scale)
+    assert_attention_close(got, want)
+    assert np.all(got[1, :, 2:] == 0) and np.all(got[2, :, 1:] == 0)
