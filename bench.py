@@ -1,0 +1,317 @@
+"""Benchmark of the paged-KV decode hot path on one MI355X.
+
+Default workload: config C2 of BASELINE.json -- one Llama-3-8B-shaped attention
+layer over int8 (G64) paged KV, B=32 sequences with context lengths drawn from
+U[1024, 8192] (seed 1).  One step = append-quantize one new K/V token per
+sequence + paged attention of the new query over all L_b + 1 tokens.
+
+Steps rotate over ``--layers`` independent layer pools (default 4, ~1.3 GB of
+KV) so that a step never finds its KV in the 256 MB Infinity Cache, the same
+access pattern a 32-layer model has.  Inputs are synthetic and resident in HBM
+before timing.  Prints one JSON line (rank 0).
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "mlx-one_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+
+def kv_bytes_per_token(w):
+    """K+V bytes of one cached token: 2*HK*(D*bits/8 + (D/G)*4), or 2*HK*D*2 for bf16."""
+    if w.bits == 16:
+        return 2 * w.kv_heads * w.head_dim * 2
+    return 2 * w.kv_heads * (w.head_dim * w.bits // 8 + (w.head_dim // w.group_size) * 4)
+
+
+def algorithmic_bytes(w, lengths):
+    """Algorithmic bytes of the attention launch and of the whole step.
+
+    ``lengths`` are the tokens attended per sequence (after the append).
+    Attention: every cached token's K/V once, queries and outputs (bf16), one
+    4-byte block-table entry per page.  Step (the C2 formula):
+    attention + the new bf16 K/V rows the append reads.
+    """
+    tokens = float(sum(lengths))
+    kv = kv_bytes_per_token(w) * tokens
+    qo = w.batch * w.heads * w.num_queries * w.head_dim * 2 * 2
+    table = 4 * sum(math.ceil(x / w.page_tokens) for x in lengths)
+    attention = kv + qo + table
+    new_rows = w.batch * w.append_tokens * 2 * w.kv_heads * w.head_dim * 2
+    return attention, attention + new_rows
+
+
+class Layer:
+    """One layer's page pool, filled with the workload's context tokens."""
+
+    def __init__(self, w, inst, index, fmt, device):
+        import numpy as np
+        import torch
+
+        from pkv import ops
+
+        self.fmt = fmt
+        self.pool = ops.allocate_pool(fmt, inst.num_pages, device)
+        self.table = torch.from_numpy(inst.table).to(device)
+        gen = torch.Generator(device=device)
+        gen.manual_seed(1000 * w.seed + index)
+        rng = np.random.default_rng([w.seed, index, 7])
+        channels = w.kv_heads * w.head_dim
+        picks = []
+        for _ in range(2):
+            count = max(1, int(round(w.outlier_fraction * channels))) if w.outlier_fraction else 0
+            pick = rng.choice(channels, count, replace=False) if count else np.zeros(0, np.int64)
+            picks.append(np.divmod(pick, w.head_dim))
+        lengths = inst.context.astype(np.int64)
+        chunk = 256
+        for start in range(0, int(lengths.max()), chunk):
+            width = np.clip(lengths - start, 0, chunk).astype(np.int32)
+            kv = []
+            for side in range(2):
+                x = torch.randn((w.batch, w.kv_heads, chunk, w.head_dim), generator=gen,
+                                device=device, dtype=torch.float32)
+                hk, d = picks[side]
+                if len(hk):
+                    x[:, torch.from_numpy(hk).to(device), :, torch.from_numpy(d).to(device)] *= (
+                        w.outlier_scale)
+                kv.append(x.to(fmt.dtype))
+            ops.append_quantize(fmt, self.pool, kv[0], kv[1], self.table,
+                                torch.full((w.batch,), start, dtype=torch.int32, device=device),
+                                torch.from_numpy(width).to(device))
+        self.new_k = torch.randn((w.batch, w.kv_heads, w.append_tokens, w.head_dim),
+                                 generator=gen, device=device).to(fmt.dtype)
+        self.new_v = torch.randn((w.batch, w.kv_heads, w.append_tokens, w.head_dim),
+                                 generator=gen, device=device).to(fmt.dtype)
+        self.queries = torch.from_numpy(inst.queries).to(device=device, dtype=fmt.dtype)
+        self.out = torch.empty_like(self.queries)
+
+
+def cpu_baseline(w, inst, layer, device, budget_s):
+    """Time the oracle's C restatement of the reference algorithm on this host.
+
+    Runs the whole step for as many sequences as fit the time budget (all of
+    them for C2) on reference-format pages copied out of the GPU pool, with
+    every host core.  Also returns the max/mean abs difference between the GPU
+    output of the same step and the oracle's on the sampled sequences.
+    """
+    import numpy as np
+    import torch
+
+    from oracle import cport
+    from pkv import ops
+
+    fmt = layer.fmt
+    cores = len(os.sched_getaffinity(0))
+    used = sorted({int(p) for p in inst.table.ravel() if p >= 0})
+    pages = ops.gather_pages(fmt, layer.pool, used)
+    torch.cuda.synchronize()
+    num = inst.num_pages
+    host = []
+    for t in pages:
+        a = t.view(torch.int16).cpu().numpy().view(np.uint16) if t.element_size() == 2 else t.cpu().numpy()
+        full = np.zeros((num,) + a.shape[1:], a.dtype)
+        full[used] = a
+        host.append(full)
+    lengths = inst.context + w.append_tokens
+    positions = (lengths - 1).reshape(-1, 1).astype(np.int32)
+    widths = np.ones(w.batch, np.int32)
+    q = layer.queries.float().cpu().numpy()
+    scale = 1.0 / math.sqrt(w.head_dim)
+
+    new = np.random.default_rng(0).standard_normal(
+        (w.batch * w.kv_heads * 2 * max(w.append_tokens, 1), w.head_dim)).astype(np.float32)
+
+    def run(rows):
+        sub = slice(0, rows)
+        if w.bits != 16 and w.append_tokens:
+            cport.quantize_rows(new[:rows * w.kv_heads * 2 * w.append_tokens], w.bits, w.group_size)
+        return cport.paged_attention(q[sub], inst.table[sub], lengths[sub], positions[sub],
+                                     widths[sub], heads_kv=w.kv_heads, page_tokens=w.page_tokens,
+                                     bits=w.bits, group_size=w.group_size, pages=host,
+                                     scale=scale, threads=cores)
+
+    started = time.perf_counter()
+    want = run(w.batch)                       # warm-up and a full-step reference
+    first = time.perf_counter() - started
+    rows = w.batch
+    reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run(rows)
+        times.append(time.perf_counter() - t0)
+    step_s = float(np.median(times))
+    return {"value": rows / step_s, "unit": "seqs*tok/s", "cores": cores, "kind": "port",
+            "sample": f"full {w.name} step ({rows} sequences, 1 layer: quantize the new K/V "
+                      f"rows + attention over {int(lengths.sum())} cached tokens), median of "
+                      f"{reps}, OpenMP C restatement (oracle/pkv_oracle.c) on "
+                      f"reference-format pages",
+            "ms_per_step": step_s * 1e3}, want
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--workload", default="c2")
+    parser.add_argument("--layers", type=int, default=4)
+    parser.add_argument("--split-tokens", type=int, default=0)
+    parser.add_argument("--graph", action="store_true",
+                        help="replay the timed steps as one captured HIP graph")
+    parser.add_argument("--cpu-budget", type=float, default=15.0,
+                        help="seconds of CPU baseline timing (0 disables)")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the paged decode path "
+                          "shards by sequence with no exchange; run with --gpus 1"}))
+        return 2
+
+    import numpy as np
+    import torch
+
+    from pkv import _native, ops, workloads
+
+    _native.load()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    w = workloads.get(args.workload)
+    total_steps = args.warmup + args.steps
+    growth = math.ceil(total_steps / args.layers) * w.append_tokens
+    inst = workloads.generate(w, extra_tokens=growth, kv=False)
+    fmt = ops.PageFormat(w.kv_heads, w.head_dim, w.page_tokens, w.bits, w.group_size,
+                         torch.bfloat16)
+    layers = [Layer(w, inst, i, fmt, device) for i in range(args.layers)]
+    torch.cuda.synchronize()
+
+    context = inst.context.astype(np.int64)
+    scale = 1.0 / math.sqrt(w.head_dim)
+    split, _ = ops.plan_partitions(context + w.append_tokens, w.page_tokens, w.kv_heads,
+                                   args.split_tokens or w.split_tokens)
+    # per-step device arrays (no host->device copies inside the timed loop)
+    plans = []
+    for s in range(total_steps):
+        li = s % args.layers
+        start = context + (s // args.layers) * w.append_tokens
+        lens = start + w.append_tokens
+        _, units = ops.plan_partitions(lens, w.page_tokens, w.kv_heads, split)
+        plans.append((li, torch.from_numpy(start.astype(np.int32)).to(device),
+                      torch.from_numpy(lens.astype(np.int32)).to(device), units,
+                      [int(x) for x in lens]))
+    max_units = max(p[3] for p in plans)
+    workspace = torch.empty(max(ops.workspace_bytes(fmt, w.heads, w.num_queries, max_units), 1),
+                            dtype=torch.uint8, device=device)
+
+    lib = _native.load()
+    layout = fmt.c_layout
+    stream = torch.cuda.current_stream(device)
+
+    def step(s, ev=None):
+        li, start, lens, units, _ = plans[s]
+        layer = layers[li]
+        h = _native.stream_handle(device)
+        if w.append_tokens:
+            code = lib.pkv_append_quantize(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
+                                           layer.new_k.data_ptr(), layer.new_v.data_ptr(), w.batch,
+                                           w.append_tokens, layer.table.data_ptr(),
+                                           layer.table.shape[1], start.data_ptr(), None, None)
+            if code:
+                _native.check(code, "append")
+        if ev is not None:
+            ev[0].record(stream)
+        code = lib.pkv_paged_attention(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
+                                       layer.queries.data_ptr(), w.batch, w.heads, w.num_queries,
+                                       layer.table.data_ptr(), layer.table.shape[1],
+                                       lens.data_ptr(), None, None, scale, split, units,
+                                       workspace.data_ptr(), workspace.numel(),
+                                       layer.out.data_ptr())
+        if ev is not None:
+            ev[1].record(stream)
+        if code:
+            _native.check(code, "attention")
+
+    # first step checked against the oracle below (before warm-up mutates the pools)
+    check_step = None
+    if args.cpu_budget > 0:
+        step(0)
+        torch.cuda.synchronize()
+        check_step = layers[0].out.float().cpu().numpy()
+        # undo nothing: the appended token is re-written identically by later steps
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    if args.graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(args.steps):
+                step(args.warmup + i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        attn_ms = None
+    else:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(args.warmup + i, events[i])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    ms_per_step = wall / args.steps * 1e3
+    timed = plans[args.warmup:]
+    mean_lens = np.mean([p[4] for p in timed], axis=0)
+    attn_bytes, step_bytes = algorithmic_bytes(w, mean_lens)
+    value = w.batch / (ms_per_step / 1e3)
+    roofline = None
+    if attn_ms:
+        achieved = attn_bytes / (attn_ms / 1e3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
+                    "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
+    result = {
+        "metric": "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)",
+        "value": round(value, 1), "unit": "seqs*tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8" if w.bits == 8 else f"u{w.bits}",
+        "data": "synthetic",
+        "config": {"workload": w.name, "batch": w.batch, "heads": w.heads,
+                   "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
+                   "bits": w.bits, "group_size": w.group_size, "mean_context": float(mean_lens.mean()),
+                   "split_tokens": split, "layers_rotated": args.layers, "graph": args.graph},
+        "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
+        "roofline": roofline,
+    }
+    if args.cpu_budget > 0:
+        base, want = cpu_baseline(w, inst, layers[0], device, args.cpu_budget)
+        got = check_step
+        # The oracle reads the pool after all steps; later steps only wrote
+        # positions past step 0's lengths, which the oracle does not read.
+        err = np.abs(got - workloads.bf16_round(want.reshape(got.shape)))
+        base["check_vs_gpu"] = {"max_abs": float(err.max()), "mean_abs": float(err.mean())}
+        result["cpu_baseline"] = base
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -47,6 +47,19 @@ struct Cfg {
   static constexpr int CS = LB < 16 ? LB : 16;
   static constexpr int NCH = LB / CS;
   static constexpr int MW = QUANT ? 4 * NG : 1;  // meta dwords per lane (4 tokens x NG)
+  // LDS ring slot of one tile: [K payload][V payload][K meta][V meta]
+  static constexpr int KP = LB * 64;
+  static constexpr int META = QUANT ? 128 * NG : 0;
+  static constexpr int SLOT = 2 * KP + META;
+  // tiles per wave ring (NBUF - 1 in flight): about 13 KB of LDS per wave, so
+  // three 4-wave workgroups fit a CU's 160 KB
+  static constexpr int NBUF_RAW = 13312 / SLOT;
+  static constexpr int NBUF = NBUF_RAW < 2 ? 2 : NBUF_RAW > 8 ? 8 : NBUF_RAW;
+  // LDS-DMA instructions per tile (each decrements vmcnt once)
+  static constexpr int PAY_INSTS = CS == 16 ? NCH : 2;
+  static constexpr int META_INSTS = QUANT ? (32 * NG + 63) / 64 : 0;
+  static constexpr int LPT = 2 * PAY_INSTS + META_INSTS;
+  static_assert((NBUF - 1) * LPT <= 63, "vmcnt range");
 };
 
 template <typename C>
@@ -57,32 +70,99 @@ struct Tile {
   uint32_t vm[C::MW];
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Global -> LDS DMA of one 16- or 4-byte piece per lane: lane l's data lands
+// at dst + l*size (dst is wave-uniform).
+__device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *src, uint8_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 4, 0, 0);
+}
+
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= VM only.
+template <int VM>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Wait until the tile that has `younger` tiles issued after it has landed
+// (DMA groups complete in issue order).
+template <typename C, int K>
+__device__ __forceinline__ void wait_tile_rec(int younger) {
+  if constexpr (K == 0) {
+    wait_vm<0>();
+  } else {
+    if (younger >= K) wait_vm<K * C::LPT>();
+    else wait_tile_rec<C, K - 1>(younger);
+  }
+}
 template <typename C>
-__device__ __forceinline__ void load_payload(uint32_t (&w)[C::LW], const uint8_t *tile, int lane) {
+__device__ __forceinline__ void wait_tile(int younger) {
+  wait_tile_rec<C, C::NBUF - 1>(younger);
+}
+
+// Issue the LDS-DMA of one 16-token tile (payload chunks + metadata words).
+template <typename C>
+__device__ __forceinline__ void issue_tile(uint8_t *slot, const AttnArgs &a, const uint8_t *head,
+                                           int tile_in_page, int lane) {
+  const int64_t off = (int64_t)tile_in_page * a.g.tile_bytes;
+  const uint8_t *kt = head + off, *vt = head + a.g.v_offset + off;
   if constexpr (C::CS == 16) {
 #pragma unroll
-    for (int c = 0; c < C::NCH; ++c) {
-      u4 x = __builtin_nontemporal_load((const u4 *)(tile + c * 1024 + lane * 16));
-      w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
-    }
+    for (int c = 0; c < C::NCH; ++c) dma16(kt + c * 1024 + lane * 16, slot + c * 1024);
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) dma16(vt + c * 1024 + lane * 16, slot + C::KP + c * 1024);
   } else {
-    u2 x = __builtin_nontemporal_load((const u2 *)(tile + lane * 8));
-    w[0] = x.x; w[1] = x.y;
+    dma4(kt + lane * 8, slot);
+    dma4(kt + lane * 8 + 4, slot + 256);
+    dma4(vt + lane * 8, slot + C::KP);
+    dma4(vt + lane * 8 + 4, slot + C::KP + 256);
+  }
+  if constexpr (C::QUANT) {
+    const int base = tile_in_page * PKV_TILE * C::NG;
+#pragma unroll
+    for (int m = 0; m < 32 * C::NG; m += 64) {
+      const int idx = m + lane;
+      if (idx < 32 * C::NG) {
+        const uint8_t *src = idx < 16 * C::NG
+                                 ? head + a.g.kmeta_offset + (int64_t)(base + idx) * 4
+                                 : head + a.g.vmeta_offset + (int64_t)(base + idx - 16 * C::NG) * 4;
+        dma4(src, slot + 2 * C::KP + m * 4);
+      }
+    }
   }
 }
 
+// Registers of one tile from its LDS slot: lane payload and the lane's 4 tokens' meta.
 template <typename C>
-__device__ __forceinline__ void load_tile(Tile<C> &t, const AttnArgs &a, const uint8_t *head,
-                                          int tile_in_page, int lane, int jj) {
-  const int64_t off = (int64_t)tile_in_page * a.g.tile_bytes;
-  load_payload<C>(t.k, head + off, lane);
-  load_payload<C>(t.v, head + a.g.v_offset + off, lane);
-  if constexpr (C::QUANT) {
-    const int tok = tile_in_page * PKV_TILE + 4 * jj;
-    const uint32_t *km = (const uint32_t *)(head + a.g.kmeta_offset) + tok * C::NG;
-    const uint32_t *vm = (const uint32_t *)(head + a.g.vmeta_offset) + tok * C::NG;
+__device__ __forceinline__ void read_tile(Tile<C> &t, const uint8_t *slot, int lane, int jj) {
+  if constexpr (C::CS == 16) {
 #pragma unroll
-    for (int i = 0; i < C::MW; ++i) { t.km[i] = km[i]; t.vm[i] = vm[i]; }
+    for (int c = 0; c < C::NCH; ++c) {
+      const u4 x = *(const u4 *)(slot + c * 1024 + lane * 16);
+      const u4 y = *(const u4 *)(slot + C::KP + c * 1024 + lane * 16);
+      t.k[4 * c] = x.x; t.k[4 * c + 1] = x.y; t.k[4 * c + 2] = x.z; t.k[4 * c + 3] = x.w;
+      t.v[4 * c] = y.x; t.v[4 * c + 1] = y.y; t.v[4 * c + 2] = y.z; t.v[4 * c + 3] = y.w;
+    }
+  } else {
+    t.k[0] = *(const uint32_t *)(slot + lane * 4);
+    t.k[1] = *(const uint32_t *)(slot + 256 + lane * 4);
+    t.v[0] = *(const uint32_t *)(slot + C::KP + lane * 4);
+    t.v[1] = *(const uint32_t *)(slot + C::KP + 256 + lane * 4);
+  }
+  if constexpr (C::QUANT) {
+    const uint32_t *km = (const uint32_t *)(slot + 2 * C::KP) + 4 * jj * C::NG;
+    const uint32_t *vm = km + 16 * C::NG;
+#pragma unroll
+    for (int i = 0; i < C::MW; i += 4) {
+      const u4 x = *(const u4 *)(km + i);
+      const u4 y = *(const u4 *)(vm + i);
+      t.km[i] = x.x; t.km[i + 1] = x.y; t.km[i + 2] = x.z; t.km[i + 3] = x.w;
+      t.vm[i] = y.x; t.vm[i + 1] = y.y; t.vm[i + 2] = y.z; t.vm[i + 3] = y.w;
+    }
   }
 }
 
@@ -173,7 +253,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   using KT = typename FO::KT;
   using VT = typename FO::VT;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, jj = lane >> 4;
   const int w = blockIdx.x * 4 + wave;
   if (w >= a.max_units) return;
@@ -181,6 +262,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   const int kh = w % g.hk, su = w / g.hk;
   int b, part, nsplit, first_unit;
   if (!locate_unit(a.seq_lens, a.batch, a.split, su, lane, b, part, nsplit, first_unit)) return;
+  // wave-uniform values live in SGPRs: scalar branches, scalar loads
+  b = __builtin_amdgcn_readfirstlane(b);
+  part = __builtin_amdgcn_readfirstlane(part);
+  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
   const int L = a.seq_lens[b];
   const int t0 = part * a.split;
   const int t1 = min(L, t0 + a.split);
@@ -262,18 +347,16 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   } else if (lane < npages) {
     pid = -1;
   }
-  const int tiles_per_page = g.page / PKV_TILE;
+  // partitions start on page boundaries: tile -> (page, tile in page) by shifts
+  const int tpp_shift = __builtin_ctz(g.page / PKV_TILE);
   const int ntiles = t1 > t0 ? (t1 - t0 + PKV_TILE - 1) / PKV_TILE : 0;
 
   auto head_of = [&](int tile, int &tip) -> const uint8_t * {
-    const int tok = t0 + tile * PKV_TILE;
-    const int page_local = tok / g.page - first_page;
-    tip = (tok % g.page) / PKV_TILE;
-    const int id = __builtin_amdgcn_readlane(pid, page_local);
+    tip = tile & ((1 << tpp_shift) - 1);
+    const int id = __builtin_amdgcn_readlane(pid, tile >> tpp_shift);
     if (id < 0) return nullptr;
     return a.pool + (int64_t)id * g.page_bytes + (int64_t)kh * g.head_bytes;
   };
-  (void)tiles_per_page;
 
   const h4 ones = h4{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
@@ -339,7 +422,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
           tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
           tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
           const float mn = fmaxf(m[rb], tm);
-          const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[rb] - mn);
+          const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[rb] - mn);
           m[rb] = mn;
           lsum[rb] *= alpha;
 #pragma unroll
@@ -361,7 +444,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = tok0 + 4 * jj + r;
-          p[rb][r] = t <= lim[rb] ? exp2f(s[rb][r] - m[rb]) : 0.0f;
+          p[rb][r] = t <= lim[rb] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
         }
         lsum[rb] += (p[rb][0] + p[rb][1]) + (p[rb][2] + p[rb][3]);
       }
@@ -411,30 +494,39 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     }
   };
 
-  // Ping-pong over two register buffers: the next tile's loads are in flight
-  // while the current one is computed.
-  Tile<C> buf_a, buf_b;
-  bool have_a = false, have_b = false;
-  int tip = 0;
-  if (ntiles > 0) {
-    const uint8_t *h = head_of(0, tip);
-    have_a = h != nullptr;
-    if (have_a) load_tile<C>(buf_a, a, h, tip, lane, jj);
-  }
-  for (int tile = 0; tile < ntiles; tile += 2) {
-    if (tile + 1 < ntiles) {
-      const uint8_t *h = head_of(tile + 1, tip);
-      have_b = h != nullptr;
-      if (have_b) load_tile<C>(buf_b, a, h, tip, lane, jj);
+  // LDS ring of NBUF tile slots per wave, filled by DMA NBUF - 1 tiles ahead.
+  __shared__ __attribute__((aligned(16))) uint8_t ring[4][C::NBUF][C::SLOT];
+  uint8_t(*slots)[C::SLOT] = ring[wave];
+  int valid = 0;  // bit s: slot s holds a tile of a valid page
+  auto issue = [&](int tile) __attribute__((always_inline)) {
+    int tip;
+    const uint8_t *h = head_of(tile, tip);
+    const int s = tile % C::NBUF;
+    if (h) {
+      valid |= 1 << s;
+    } else {
+      // keep one DMA group per tile so vmcnt accounting stays exact
+      valid &= ~(1 << s);
+      h = a.pool + (int64_t)kh * g.head_bytes;
+      tip = 0;
     }
-    if (have_a) process(buf_a, tile);
-    if (tile + 1 < ntiles) {
-      if (tile + 2 < ntiles) {
-        const uint8_t *h = head_of(tile + 2, tip);
-        have_a = h != nullptr;
-        if (have_a) load_tile<C>(buf_a, a, h, tip, lane, jj);
-      }
-      if (have_b) process(buf_b, tile + 1);
+    issue_tile<C>(slots[s], a, h, tip, lane);
+  };
+#pragma unroll
+  for (int p = 0; p < C::NBUF - 1; ++p)
+    if (p < ntiles) issue(p);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    // refill the slot tile-1 used; its LDS reads have completed
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    if (tile + C::NBUF - 1 < ntiles) issue(tile + C::NBUF - 1);
+    wait_tile<C>(min(ntiles - 1 - tile, C::NBUF - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const int s = tile % C::NBUF;
+    if (valid & (1 << s)) {
+      Tile<C> cur;
+      read_tile<C>(cur, slots[s], lane, jj);
+      process(cur, tile);
     }
   }
 
@@ -492,11 +584,17 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 // domain): one wave per (sequence, KV head).
 
 __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int w = blockIdx.x * 4 + wave;
-  if (w >= a.batch * a.hk) return;
-  const int b = w / a.hk, kh = w % a.hk;
-  // first unit of sequence b
+  // one wave per (sequence, KV head, query row)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t w = (int64_t)blockIdx.x * 4 + wave;
+  if (w >= (int64_t)a.batch * a.hk * a.rows) return;
+  const int row = (int)(w % a.rows);
+  const int kh = (int)((w / a.rows) % a.hk);
+  const int b = (int)(w / ((int64_t)a.rows * a.hk));
+  const int nsplit = splits_of(a.seq_lens[b], a.split);
+  if (nsplit <= 1) return;
+  // first unit of sequence b: prefix sum of the partition counts
   int carry = 0, first = 0;
   for (int c0 = 0; c0 < a.batch; c0 += 64) {
     const int idx = c0 + lane;
@@ -505,41 +603,70 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     if (b >= c0 && b < c0 + 64) first = __shfl(incl - ns, b - c0, 64);
     carry = __shfl(incl, 63, 64);
   }
-  const int nsplit = splits_of(a.seq_lens[b], a.split);
   // partitions past the launched units were never computed: never read them
-  if (nsplit <= 1 || first + nsplit > a.max_units) return;
-  for (int row = 0; row < a.rows; ++row) {
-    const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-    float top = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) {
-      const int64_t u = (int64_t)(first + s) * a.hk + kh;
-      const float ms = a.part_ml[(u * a.rows + row) * 2];
-      const float ls = a.part_ml[(u * a.rows + row) * 2 + 1];
-      if (ls > 0.0f) top = fmaxf(top, ms);
-    }
-    float norm = 0.0f;
-    float acc[4] = {0, 0, 0, 0};
-    for (int s = 0; s < nsplit; ++s) {
-      const int64_t u = (int64_t)(first + s) * a.hk + kh;
-      const float ms = a.part_ml[(u * a.rows + row) * 2];
-      const float ls = a.part_ml[(u * a.rows + row) * 2 + 1];
-      if (!(ls > 0.0f)) continue;
-      const float wgt = exp2f(ms - top);
-      norm += ls * wgt;
-      const float *pa = a.part_acc + (u * a.rows + row) * a.dp;
+  if (first + nsplit > a.max_units) return;
+  const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
+  auto unit = [&](int s) { return ((int64_t)(first + s) * a.hk + kh) * a.rows + row; };
+  // global max over live partitions (lanes stride the partitions)
+  __shared__ float s_w[4][64];
+  float top = -INFINITY;
+  for (int s = lane; s < nsplit; s += 64) {
+    const float ms = a.part_ml[unit(s) * 2], ls = a.part_ml[unit(s) * 2 + 1];
+    if (ls > 0.0f) top = fmaxf(top, ms);
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < a.dp) acc[i] += wgt * pa[d];
+  for (int o = 32; o > 0; o >>= 1) top = fmaxf(top, __shfl_xor(top, o, 64));
+  float norm = 0.0f;
+  float acc[4] = {0, 0, 0, 0};
+  const int per_lane = (a.dp + 63) / 64;
+  for (int s0 = 0; s0 < nsplit; s0 += 64) {
+    const int s = s0 + lane;
+    float wgt = 0.0f, ls = 0.0f;
+    if (s < nsplit) {
+      const float ms = a.part_ml[unit(s) * 2];
+      ls = a.part_ml[unit(s) * 2 + 1];
+      wgt = ls > 0.0f ? exp2f(ms - top) : 0.0f;  // dead partitions hold acc = 0
+    }
+    norm += wgt * ls;
+    s_w[wave][lane] = wgt;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int count = min(64, nsplit - s0);
+    // independent loads: each lane owns per_lane consecutive d of every partition
+    int j = 0;
+    for (; j + 4 <= count; j += 4) {
+      float v[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float *pa = a.part_acc + unit(s0 + j + u) * a.dp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[u][i] = i < per_lane ? pa[lane * per_lane + i] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wj = s_w[wave][j + u];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += wj * v[u][i];
       }
     }
-    const float inv = 1.0f / fmaxf(norm, 1e-20f);
-    const int64_t obase = (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
+    for (; j < count; ++j) {
+      const float *pa = a.part_acc + unit(s0 + j) * a.dp;
+      const float wj = s_w[wave][j];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane + 64 * i;
-      if (d < a.dim) a.out[obase + d] = float_to_bits(acc[i] * inv, a.float_kind);
+      for (int i = 0; i < 4; ++i)
+        if (i < per_lane) acc[i] += wj * pa[lane * per_lane + i];
     }
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) norm += __shfl_xor(norm, o, 64);
+  const float inv = 1.0f / fmaxf(norm, 1e-20f);
+  const int64_t obase = (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane * per_lane + i;
+    if (i < per_lane && d < a.dim) a.out[obase + d] = float_to_bits(acc[i] * inv, a.float_kind);
   }
 }
 
@@ -581,7 +708,7 @@ hipError_t launch_attention(hipStream_t stream, const AttnArgs &a, int row_block
 }
 
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a) {
-  const int waves = a.batch * a.hk;
+  const int64_t waves = (int64_t)a.batch * a.hk * a.rows;
   if (waves == 0) return hipSuccess;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, a);
   return hipGetLastError();

@@ -25,6 +25,8 @@ FLAGS = [
     "-fno-fast-math", "-ffp-contract=fast-honor-pragmas",
     # no packed-f32 VALU instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: no AGPR<->VGPR copies around the online softmax
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result",
 ]
 

@@ -93,8 +93,12 @@ class Instance:
             np.int32)
 
 
-def generate(w: Workload, *, extra_tokens=0, layer=0):
-    """Draw one instance; ``extra_tokens`` reserves pages for later decode steps."""
+def generate(w: Workload, *, extra_tokens=0, layer=0, kv=True):
+    """Draw one instance; ``extra_tokens`` reserves pages for later decode steps.
+
+    ``kv=False`` stops after the queries (lengths, table and queries only), for
+    callers that draw K/V on the device.
+    """
     rng = np.random.default_rng(w.seed if layer == 0 else [w.seed, layer])
     if w.lengths:
         context = np.asarray(w.lengths, np.int64)
@@ -123,6 +127,8 @@ def generate(w: Workload, *, extra_tokens=0, layer=0):
         table[b, :n] = ids
     queries = bf16_round(rng.standard_normal((w.batch, w.heads, w.num_queries, w.head_dim),
                                              dtype=np.float32))
+    if not kv:
+        return Instance(w, context.astype(np.int32), table, queries, [], [], arena)
     keys = [rng.standard_normal((w.kv_heads, int(n), w.head_dim), dtype=np.float32) for n in total]
     values = [rng.standard_normal((w.kv_heads, int(n), w.head_dim), dtype=np.float32)
               for n in total]

@@ -109,8 +109,15 @@ void pkvo_quantize_rows(const float *x, int64_t rows, int dim, int bits, int gro
     int ngroups = padded / group;
     int levels = (1 << bits) - 1;
     int bytes = bits == 4 ? padded / 2 : padded;
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+    {
     float *row = (float *)malloc(sizeof(float) * (size_t)padded);
     uint8_t *code = (uint8_t *)malloc((size_t)padded);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
     for (int64_t r = 0; r < rows; ++r) {
         const float *src = x + r * dim;
         for (int d = 0; d < padded; ++d)
@@ -146,6 +153,7 @@ void pkvo_quantize_rows(const float *x, int64_t rows, int dim, int bits, int gro
     }
     free(row);
     free(code);
+    }
 }
 
 /* ---- paged attention: paged_attention.py:209-246 --------------------- */
