@@ -1,0 +1,147 @@
+"""CPU: libpkv.so loads, exports every symbol include/pkv.h declares, validates inputs.
+
+Only host-side paths run here (layout arithmetic and argument validation return
+before any HIP call); the kernels are exercised by the ``gpu`` tests.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from pkv import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pkv.h"
+FAKE = ctypes.c_void_p(4096)   # never dereferenced: validation fails or returns first
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pkv_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_exported_and_bound():
+    lib = nat.load()
+    names = declared()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in pkv.h but not exported"
+    assert set(names) == set(nat.SIGNATURES), "ctypes bindings differ from the header"
+
+
+def test_version_and_error_text():
+    lib = nat.load()
+    assert lib.pkv_version() >= 1
+    assert isinstance(nat.last_error(), str)
+
+
+def _layout(**kw):
+    base = dict(num_kv_heads=8, head_dim=128, page_tokens=16, bits=8, group_size=64, float_kind=0)
+    base.update(kw)
+    return nat.Layout(*base.values())
+
+
+@pytest.mark.parametrize("kw,page_bytes,dim", [
+    ({}, 8 * (2 * 16 * 128 + 2 * 16 * 2 * 4), 128),                          # C2 page: 34 KiB
+    (dict(num_kv_heads=4, page_tokens=32, bits=4), 4 * (2 * 32 * 64 + 2 * 32 * 2 * 4), 128),  # C3
+    (dict(num_kv_heads=2, head_dim=64, bits=16, group_size=32), 2 * 2 * 16 * 64 * 2, 64),      # C1
+    (dict(head_dim=37, group_size=32), 8 * (2 * 16 * 64 + 2 * 16 * 2 * 4), 64),  # padded head dim
+    (dict(head_dim=256, group_size=128), 8 * (2 * 16 * 256 + 2 * 16 * 2 * 4), 256),
+])
+def test_page_geometry(kw, page_bytes, dim):
+    lib = nat.load()
+    layout = _layout(**kw)
+    assert lib.pkv_page_bytes(layout) == page_bytes
+    assert lib.pkv_stored_dim(layout) == dim
+
+
+@pytest.mark.parametrize("kw", [dict(bits=5), dict(head_dim=0), dict(head_dim=300),
+                                dict(page_tokens=24), dict(page_tokens=8), dict(group_size=16),
+                                dict(float_kind=2), dict(num_kv_heads=0)])
+def test_invalid_layouts_are_rejected(kw):
+    lib = nat.load()
+    assert lib.pkv_page_bytes(_layout(**kw)) < 0
+    assert lib.pkv_stored_dim(_layout(**kw)) < 0
+
+
+def test_workspace_size():
+    lib = nat.load()
+    # 100 partitions x 8 KV heads x 4 rows x (128 floats + 2 floats)
+    need = lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 100)
+    assert need >= 100 * 8 * 4 * (128 + 2) * 4
+
+
+def _attention(lib, layout, **kw):
+    args = dict(stream=None, pool=FAKE, num_pages=10, q=FAKE, batch=2, heads=32, nq=1, table=FAKE,
+                max_pages=4, lens=FAKE, q_pos=None, widths=None, scale=0.1, split=0, units=2,
+                ws=None, ws_bytes=0, out=FAKE)
+    args.update(kw)
+    return lib.pkv_paged_attention(args["stream"], layout, args["pool"], args["num_pages"],
+                                   args["q"], args["batch"], args["heads"], args["nq"],
+                                   args["table"], args["max_pages"], args["lens"], args["q_pos"],
+                                   args["widths"], args["scale"], args["split"], args["units"],
+                                   args["ws"], args["ws_bytes"], args["out"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(heads=30), nat.PKV_UNSUPPORTED),                      # not a GQA multiple of HK=8
+    (dict(nq=9), nat.PKV_UNSUPPORTED),                          # 9 x 4 = 36 rows > 32
+    (dict(pool=None), nat.PKV_INVALID_ARGUMENT),
+    (dict(split=24), nat.PKV_INVALID_ARGUMENT),                 # not a page multiple
+    (dict(split=16 * 65), nat.PKV_INVALID_ARGUMENT),            # more than 64 pages
+    (dict(units=1), nat.PKV_INVALID_ARGUMENT),                  # fewer units than sequences
+    (dict(units=3), nat.PKV_OUT_OF_MEMORY),                     # split-K needs a workspace
+    (dict(scale=float("inf")), nat.PKV_INVALID_ARGUMENT),
+    (dict(batch=-1), nat.PKV_INVALID_ARGUMENT),
+    (dict(batch=0), nat.PKV_OK),
+])
+def test_attention_argument_validation(kw, code):
+    lib = nat.load()
+    assert _attention(lib, _layout(), **kw) == code
+    if code != nat.PKV_OK:
+        assert nat.last_error()
+
+
+def test_append_argument_validation():
+    lib = nat.load()
+    layout = _layout()
+    call = lambda **kw: lib.pkv_append_quantize(
+        None, layout, kw.get("pool", FAKE), 10, FAKE, FAKE, kw.get("batch", 2), 1, FAKE, 4,
+        kw.get("start", FAKE), None, kw.get("new_lens", None))
+    assert call(pool=None) == nat.PKV_INVALID_ARGUMENT
+    assert call(start=None) == nat.PKV_INVALID_ARGUMENT
+    assert call(new_lens=FAKE) == nat.PKV_INVALID_ARGUMENT    # aliases start_pos
+    assert call(batch=0) == nat.PKV_OK
+    assert lib.pkv_append_quantize(None, _layout(bits=3), FAKE, 10, FAKE, FAKE, 1, 1, FAKE, 4,
+                                   FAKE, None, None) == nat.PKV_UNSUPPORTED
+
+
+def test_quantize_rows_argument_validation():
+    lib = nat.load()
+    assert lib.pkv_quantize_rows(None, FAKE, 4, 128, 3, 32, 0, FAKE, FAKE, FAKE) == nat.PKV_UNSUPPORTED
+    assert lib.pkv_quantize_rows(None, FAKE, 4, 128, 8, 48, 0, FAKE, FAKE, FAKE) == nat.PKV_UNSUPPORTED
+    assert lib.pkv_quantize_rows(None, FAKE, 0, 128, 8, 32, 0, FAKE, FAKE, FAKE) == nat.PKV_OK
+    assert lib.pkv_dequantize_rows(None, FAKE, FAKE, FAKE, 4, 0, 8, 32, FAKE) == nat.PKV_INVALID_ARGUMENT
+
+
+def test_status_codes_map_to_reference_exceptions():
+    from pkv.cache_errors import CacheCapacityError
+    from pkv.modes import ModelCapabilityUnsupported
+
+    lib = nat.load()
+    _attention(lib, _layout(), heads=30)
+    with pytest.raises(ModelCapabilityUnsupported):
+        nat.check(nat.PKV_UNSUPPORTED, "attention")
+    with pytest.raises(ValueError):
+        nat.check(nat.PKV_INVALID_ARGUMENT, "attention")
+    with pytest.raises(CacheCapacityError):
+        nat.check(nat.PKV_OUT_OF_MEMORY, "attention")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(nat.NativeLibraryMissing):
+        nat.load(tmp_path / "libpkv.so")
