@@ -163,6 +163,20 @@ def cpu_baseline(w, inst, layer, device, budget_s):
             "ms_per_step": step_s * 1e3}, want
 
 
+def copy_probe():
+    """Three device-to-device copies of 256 MiB: 256 MiB read + 256 MiB written each."""
+    import torch
+
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 3}))
+    return 0
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -175,7 +189,12 @@ def main(argv=None):
                         help="replay the timed steps as one captured HIP graph")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
                         help="seconds of CPU baseline timing (0 disables)")
+    parser.add_argument("--copy-probe", action="store_true",
+                        help="only run three 256 MiB device copies (calibrates rocprofv3 "
+                             "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic)")
     args = parser.parse_args(argv)
+    if args.copy_probe:
+        return copy_probe()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the paged decode path "
                           "shards by sequence with no exchange; run with --gpus 1"}))
