@@ -177,6 +177,16 @@ def copy_probe():
     return 0
 
 
+def workload_waves(w, lengths):
+    """Waves for a workload that fixes its partition size (C3: 512-token
+    partitions): one wave per partition of every (sequence, KV head).  0 when
+    the workload leaves it to the device's capacity."""
+    if not w.split_tokens:
+        return 0
+    tiles = sum(max(1, -(-int(x) // 16)) for x in lengths) * w.kv_heads
+    return max(1, -(-tiles * 16 // w.split_tokens))
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -184,7 +194,9 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--workload", default="c2")
     parser.add_argument("--layers", type=int, default=4)
-    parser.add_argument("--split-tokens", type=int, default=0)
+    parser.add_argument("--waves", type=int, default=0,
+                        help="attention work waves (0: the workload's partition size, else the "
+                             "device's resident capacity)")
     parser.add_argument("--graph", action="store_true",
                         help="replay the timed steps as one captured HIP graph")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
@@ -219,20 +231,18 @@ def main(argv=None):
 
     context = inst.context.astype(np.int64)
     scale = 1.0 / math.sqrt(w.head_dim)
-    split, _ = ops.plan_partitions(context + w.append_tokens, w.page_tokens, w.kv_heads,
-                                   args.split_tokens or w.split_tokens)
+    waves = args.waves or workload_waves(w, context + w.append_tokens) or ops.attention_waves(
+        fmt, w.heads, w.num_queries)
     # per-step device arrays (no host->device copies inside the timed loop)
     plans = []
     for s in range(total_steps):
         li = s % args.layers
         start = context + (s // args.layers) * w.append_tokens
         lens = start + w.append_tokens
-        _, units = ops.plan_partitions(lens, w.page_tokens, w.kv_heads, split)
         plans.append((li, torch.from_numpy(start.astype(np.int32)).to(device),
-                      torch.from_numpy(lens.astype(np.int32)).to(device), units,
+                      torch.from_numpy(lens.astype(np.int32)).to(device),
                       [int(x) for x in lens]))
-    max_units = max(p[3] for p in plans)
-    workspace = torch.empty(max(ops.workspace_bytes(fmt, w.heads, w.num_queries, max_units), 1),
+    workspace = torch.empty(ops.workspace_bytes(fmt, w.heads, w.num_queries, waves),
                             dtype=torch.uint8, device=device)
 
     lib = _native.load()
@@ -240,7 +250,7 @@ def main(argv=None):
     stream = torch.cuda.current_stream(device)
 
     def step(s, ev=None):
-        li, start, lens, units, _ = plans[s]
+        li, start, lens, _ = plans[s]
         layer = layers[li]
         h = _native.stream_handle(device)
         if w.append_tokens:
@@ -255,7 +265,7 @@ def main(argv=None):
         code = lib.pkv_paged_attention(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                        layer.queries.data_ptr(), w.batch, w.heads, w.num_queries,
                                        layer.table.data_ptr(), layer.table.shape[1],
-                                       lens.data_ptr(), None, None, scale, split, units,
+                                       lens.data_ptr(), None, None, scale, waves,
                                        workspace.data_ptr(), workspace.numel(),
                                        layer.out.data_ptr())
         if ev is not None:
@@ -297,7 +307,7 @@ def main(argv=None):
         attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
     ms_per_step = wall / args.steps * 1e3
     timed = plans[args.warmup:]
-    mean_lens = np.mean([p[4] for p in timed], axis=0)
+    mean_lens = np.mean([p[3] for p in timed], axis=0)
     attn_bytes, step_bytes = algorithmic_bytes(w, mean_lens)
     value = w.batch / (ms_per_step / 1e3)
     roofline = None
@@ -305,7 +315,7 @@ def main(argv=None):
         achieved = attn_bytes / (attn_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
+                    "kernel": "pkv_paged_attention (attn_kernel, merge fused)",
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     result = {
         "metric": "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)",
@@ -316,7 +326,7 @@ def main(argv=None):
         "config": {"workload": w.name, "batch": w.batch, "heads": w.heads,
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
                    "bits": w.bits, "group_size": w.group_size, "mean_context": float(mean_lens.mean()),
-                   "split_tokens": split, "layers_rotated": args.layers, "graph": args.graph},
+                   "waves": waves, "layers_rotated": args.layers, "graph": args.graph},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
     }

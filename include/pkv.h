@@ -88,11 +88,14 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
 
 /*
  * Causal GQA paged attention for decode (num_queries = 1) and speculative
- * verify (num_queries = 1 + drafts): dequantization fused into the page load,
- * split-K over token partitions of `split_tokens`, log-sum-exp merge.
+ * verify (num_queries = 1 + drafts), dequantization fused into the page load.
  * Replaces paged_attention and its Metal kernel
  * (src/mlx_one/engine/paged_attention.py:62-124 kernel, :127-206 dispatch and
- * partition merge).
+ * partition merge).  The reference splits each sequence into fixed token
+ * partitions; here the 16-token tiles of all (sequence, KV head) pairs are
+ * shared out as equal runs over `waves` waves, and a pair whose tiles span
+ * several runs is merged by log-sum-exp (:191-204) in a second kernel on the
+ * same stream.
  *
  *  queries      : [batch][num_heads][num_queries][head_dim], float_kind
  *  seq_lens     : [batch] tokens in each sequence's cache (after the append)
@@ -101,23 +104,25 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
  *                 when t <= q_pos (paged_attention.py:81)
  *  widths       : [batch] real query rows (rows q >= widths[b] output 0), or NULL
  *  scale        : softmax scale
- *  split_tokens : tokens per partition, a multiple of page_tokens, at most
- *                 64 pages; 0 picks a default
- *  max_units    : number of (sequence, partition) pairs to launch for, at least
- *                 sum_b max(1, ceil(seq_lens[b] / split_tokens)); extra ones exit
+ *  waves        : work waves; <= 0 picks pkv_attention_waves(...)
  *  workspace    : device scratch of pkv_attention_workspace_bytes(...) bytes
+ *                 (calls sharing one workspace must not overlap)
  *  out          : [batch][num_heads][num_queries][head_dim], float_kind
  */
 int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool,
                         int64_t num_pages, const void *queries, int32_t batch,
                         int32_t num_heads, int32_t num_queries, const int32_t *block_table,
                         int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
-                        const int32_t *widths, float scale, int32_t split_tokens,
-                        int32_t max_units, void *workspace, int64_t workspace_bytes, void *out);
+                        const int32_t *widths, float scale, int32_t waves, void *workspace,
+                        int64_t workspace_bytes, void *out);
 
-/* Workspace bytes pkv_paged_attention needs for `max_units` partitions. */
+/* Waves the attention kernel keeps resident on the current device for this
+ * layout and (num_heads, num_queries): the default `waves`.  <0 on error. */
+int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries);
+
+/* Workspace bytes pkv_paged_attention needs for `waves` work waves. */
 int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
-                                      int32_t num_queries, int32_t max_units);
+                                      int32_t num_queries, int32_t waves);
 
 /*
  * Copy pages out of the pool into the reference's per-page tensor format

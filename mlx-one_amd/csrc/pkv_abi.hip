@@ -6,9 +6,13 @@
 // PKV_OUT_OF_MEMORY.  Nothing here allocates device memory or synchronises.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "pkv.h"
 
@@ -41,7 +45,38 @@ int geometry(const pkv_layout *layout, pkv_geometry *g) {
   return PKV_OK;
 }
 
-constexpr int kDefaultSplit = 256;
+// Attention workspace: [ml: S*rows*2 f32][acc: S*rows*DP f32] with
+// S = kSlotsPerWave * waves partial slots, each part 256-byte aligned.
+struct WorkspaceParts {
+  int64_t ml, acc, total;
+};
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+WorkspaceParts workspace_parts(const pkv_geometry &g, int64_t rows, int64_t waves) {
+  const int64_t slots = (int64_t)pkv::kSlotsPerWave * waves;
+  WorkspaceParts w;
+  w.ml = 0;
+  w.acc = align256(slots * rows * 2 * 4);
+  w.total = w.acc + slots * rows * g.dp * 4;
+  return w;
+}
+
+// Resident-wave capacity per (device, layout, rows), measured once.
+int cached_waves(const pkv_geometry &geo, int rows) {
+  static std::mutex mu;
+  static std::map<std::pair<int, std::string>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  char key[128];
+  snprintf(key, sizeof key, "%d/%d/%d/%d/%d/%d", geo.hk, geo.dp, geo.bits, geo.group, geo.float_kind, rows);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({dev, key});
+  if (it != cache.end()) return it->second;
+  const int w = pkv::attention_waves(pkv::to_geo(geo), rows);
+  if (w > 0) cache[{dev, key}] = w;
+  return w;
+}
 
 }  // namespace
 
@@ -92,23 +127,35 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
   return check_launch(pkv::launch_append((hipStream_t)stream, a), "append launch");
 }
 
-int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
-                                      int32_t num_queries, int32_t max_units) {
+int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries) {
   pkv_geometry g;
-  if (geometry(layout, &g) != PKV_OK || num_heads < 1 || num_queries < 1 || max_units < 0) return -1;
+  if (geometry(layout, &g) != PKV_OK) return -1;
+  if (num_heads < 1 || num_queries < 1 || num_heads % g.hk) return -1;
+  const int rows = num_queries * (num_heads / g.hk);
+  if (rows > 32) return -1;
+  const int w = cached_waves(g, rows);
+  if (w <= 0) {
+    fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
+    return -1;
+  }
+  return w;
+}
+
+int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
+                                      int32_t num_queries, int32_t waves) {
+  pkv_geometry g;
+  if (geometry(layout, &g) != PKV_OK || num_heads < 1 || num_queries < 1 || num_heads % g.hk ||
+      waves < 1)
+    return -1;
   const int64_t rows = (int64_t)num_queries * (num_heads / g.hk);
-  const int64_t units = (int64_t)max_units * g.hk;
-  const int64_t acc = units * rows * g.dp * 4;
-  const int64_t ml = units * rows * 2 * 4;
-  return (acc + 255) / 256 * 256 + ml;
+  return workspace_parts(g, rows, waves).total;
 }
 
 int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
                         const void *queries, int32_t batch, int32_t num_heads, int32_t num_queries,
                         const int32_t *block_table, int32_t max_pages, const int32_t *seq_lens,
-                        const int32_t *q_pos, const int32_t *widths, float scale,
-                        int32_t split_tokens, int32_t max_units, void *workspace,
-                        int64_t workspace_bytes, void *out) {
+                        const int32_t *q_pos, const int32_t *widths, float scale, int32_t waves,
+                        void *workspace, int64_t workspace_bytes, void *out) {
   pkv_geometry geo;
   if (int rc = geometry(layout, &geo)) return rc;
   if (batch < 0) return fail(PKV_INVALID_ARGUMENT, "negative batch");
@@ -124,20 +171,20 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
     return fail(PKV_INVALID_ARGUMENT, "paged attention requires pool, queries, block table, lengths, out");
   if (num_pages < 1 || max_pages < 1) return fail(PKV_INVALID_ARGUMENT, "empty page pool or block table");
   if (!std::isfinite(scale)) return fail(PKV_INVALID_ARGUMENT, "softmax scale must be finite");
-  int split = split_tokens > 0 ? split_tokens : (kDefaultSplit + geo.page - 1) / geo.page * geo.page;
-  if (split % geo.page || split / geo.page > 64)
-    return fail(PKV_INVALID_ARGUMENT, "split_tokens must be a multiple of page_tokens and at most 64 pages");
-  if (max_units < batch) return fail(PKV_INVALID_ARGUMENT, "max_units is below the number of sequences");
-  const int64_t need = pkv_attention_workspace_bytes(layout, num_heads, num_queries, max_units);
-  if (max_units > batch && (!workspace || workspace_bytes < need))
-    return fail(PKV_OUT_OF_MEMORY, "attention workspace too small: need " + std::to_string(need) + " bytes");
-  if ((int64_t)max_units * geo.hk > INT32_MAX)
-    return fail(PKV_INVALID_ARGUMENT, "too many partitions");
+  if (waves <= 0) {
+    waves = cached_waves(geo, rows);
+    if (waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
+  }
+  if (waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
+  // the kernel numbers 16-token tiles in int32: bound them by the block table
+  const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16);
+  if ((int64_t)batch * tiles_per_seq * geo.hk > INT32_MAX / 2)
+    return fail(PKV_UNSUPPORTED, "paged attention batch too large (more than 2^30 tiles)");
+  const WorkspaceParts parts = workspace_parts(geo, rows, waves);
+  if (!workspace || workspace_bytes < parts.total)
+    return fail(PKV_OUT_OF_MEMORY,
+                "attention workspace too small: need " + std::to_string(parts.total) + " bytes");
 
-  const int64_t units = (int64_t)max_units * geo.hk;
-  float *part_acc = (float *)workspace;
-  float *part_ml = workspace ? (float *)((char *)workspace + (units * rows * geo.dp * 4 + 255) / 256 * 256)
-                             : nullptr;
   pkv::AttnArgs a;
   a.g = pkv::to_geo(geo);
   a.pool = (const uint8_t *)pool;
@@ -154,15 +201,11 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   a.q_pos = q_pos;
   a.widths = widths;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.split = split;
-  a.max_units = (int)units;
-  a.part_acc = part_acc;
-  a.part_ml = part_ml;
+  a.waves = waves;
+  a.part_ml = (float *)((char *)workspace + parts.ml);
+  a.part_acc = (float *)((char *)workspace + parts.acc);
   a.out = (uint16_t *)out;
-  const int row_blocks = rows <= 16 ? 1 : 2;
-  if (int rc = check_launch(pkv::launch_attention((hipStream_t)stream, a, row_blocks), "attention launch"))
-    return rc;
-  if (max_units == batch) return PKV_OK;  // one partition per sequence: no merge
+  if (int rc = check_launch(pkv::launch_attention((hipStream_t)stream, a), "attention launch")) return rc;
   pkv::MergeArgs m;
   m.batch = batch;
   m.hk = geo.hk;
@@ -172,12 +215,11 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   m.rows = rows;
   m.dim = geo.dim;
   m.dp = geo.dp;
-  m.split = split;
   m.float_kind = geo.float_kind;
-  m.max_units = max_units;
+  m.waves = waves;
   m.seq_lens = seq_lens;
-  m.part_acc = part_acc;
-  m.part_ml = part_ml;
+  m.part_acc = a.part_acc;
+  m.part_ml = a.part_ml;
   m.out = (uint16_t *)out;
   return check_launch(pkv::launch_merge((hipStream_t)stream, m), "merge launch");
 }

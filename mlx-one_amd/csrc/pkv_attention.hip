@@ -5,25 +5,52 @@
 // t <= q_pos[q] of its sequence, KV head kh = h / (H/HK), softmax(q.k*scale).v,
 // normaliser floored at 1e-20, rows q >= width give 0.
 //
-// Work unit = one wave = (sequence, partition of split_tokens, KV head).  All
-// R = Q*(H/HK) query rows of the KV head share each K/V tile load (GQA reuse).
-// Per 16-token tile:
-//   S^T[t][row] = K.Q^T    v_mfma_f32_16x16x32_f16 over the codes as f16
-//                          (1024 + c, built with one v_perm per two codes);
-//                          one accumulator per quantization group, then
-//                          s = sum_g scale_g*acc_g + qsum_g*(bias_g - 1024*scale_g)
-//   softmax                exp2 domain, online with lazy rescaling: the running
-//                          max moves only when a score exceeds it by > 8
-//   O[row][d] += P'.V      v_mfma_f32_16x16x16_f16, P'_g = p*scale_v[g] (so V is
-//                          never dequantized); bias_v enters as sum p*bias_v and
-//                          the 1024 offset as 1024 * (P'.ones)
+// Work split (stream-K).  The 16-token tiles of every (sequence, KV head)
+// segment, in that order, are shared out as equal contiguous runs over a grid
+// of resident waves (one 64-thread workgroup each): no wave waits on a ragged
+// tail and each pays its start-up latency once.  A wave processes the pieces
+// of the segments its run crosses; all R = Q*(H/HK) query rows of the KV head
+// share each K/V tile load (GQA reuse).
+//
+// Column slots.  The 16 columns of a 16x16 MFMA tile hold SLOTS = 16/RPS
+// groups of RPS query rows; slot j of an iteration works on tile (SLOTS*it +
+// j).  The slot-j query operand is zero outside its columns, so the score
+// MFMAs of SLOTS tiles accumulate into one dense 16x16 tile, and every lane's
+// softmax work is useful (decode at GQA 4 would otherwise leave 12 of 16
+// columns empty).  Each column keeps its own online-softmax state, so the
+// SLOTS columns of a row are independent sub-partitions (interleaved tiles)
+// merged by log-sum-exp once per unit.
+//
+// Per iteration (SLOTS tiles of 16 tokens):
+//   S^T[t][col] = K.Q^T   v_mfma_f32_16x16x32_f16 over the codes as f16
+//                         (1024 + c, one v_perm per two codes); one
+//                         accumulator per quantization group, then
+//                         s = sum_g scale_g*acc_g + qsum_g*(bias_g - 1024*scale_g)
+//   softmax               exp2 domain, online with lazy rescaling: a column's
+//                         running max moves only when a score exceeds it by > 8
+//   O^T[d][col] += V^T.P' v_mfma_f32_16x16x16_f16 with P'_g = p*scale_v[g]
+//                         (V is never dequantized); bias_v enters as
+//                         sum p*bias_v, the 1024 offset as 1024*sum P'.
+// O is kept transposed (d in rows, columns in lanes): rescaling a column
+// touches only the lane's own registers.
+//
+// Loads.  The page format stores a lane's share of a tile where its MFMA
+// operand registers want it (16-byte chunks at tile + c*1024 + lane*16), so K
+// and V stream from HBM straight into VGPRs (global_load_dwordx4, no LDS
+// staging).  The next iteration's K and score metadata are requested as soon
+// as the score MFMAs have consumed the current ones, its V and value metadata
+// after the PV MFMAs; the other waves of the CU (one wave per workgroup, no
+// LDS, bounded VGPRs) cover the rest of the latency.
 // Float (bf16/f16) pages use the same schedule without the affine terms.
-// A unit that covers its whole sequence writes the normalised output; other
-// units write (acc, m, l) partials merged by merge_kernel.
+// A piece that covers its whole segment writes the normalised output; other
+// pieces write (acc, m, l) partials that merge_kernel, launched next on the
+// same stream, combines by log-sum-exp (the kernel boundary makes them
+// visible across the XCDs' L2s without any cache maintenance in the loop).
+#include <type_traits>
+
 #include "pkv_launch.h"
 
 namespace pkv {
-
 
 constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units)
 
@@ -36,133 +63,67 @@ constexpr uint32_t kMagic = 0x64646464u;
 constexpr uint32_t kSelLo = 0x00050004u;
 constexpr uint32_t kSelHi = 0x00070006u;
 
-template <int BITS, int DP, int G, int RB, int FK>
+// Column slots for a layout: the count the rows allow, halved while the
+// per-lane register estimate (payload of SLOTS tiles, metadata, O^T, Q) stays
+// above what leaves room for three waves per SIMD.
+constexpr int fit_slots(int bits, int dp, int g, int slots) {
+  const int lw = dp * bits / 128;
+  const int mw = bits != 16 ? 4 * (dp / g) : 0;
+  while (slots > 1 && slots * 2 * lw + 2 * mw + dp / 4 + dp / 8 + 40 > 176) slots /= 2;
+  return slots;
+}
+
+// Shapes whose register needs sit just above 256 VGPRs: asking for two waves
+// per SIMD costs them at most a few spills outside the tile loop and doubles
+// their occupancy.  Others keep the compiler's choice (heavier shapes would
+// spill inside the loop).
+constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
+  return (bits == 8 && dp == 128 && g == 64 && rb == 1 && slots == 4) ||
+                 (bits == 4 && dp == 128 && g == 32 && rb == 1 && slots == 4) ||
+                 (bits == 4 && dp == 128 && g == 64 && rb == 2) ||
+                 (bits == 8 && dp == 256 && g == 128 && rb == 1)
+             ? 2
+             : 1;
+}
+
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
 struct Cfg {
   static constexpr bool QUANT = BITS != 16;
   static constexpr int NG = QUANT ? DP / G : 1;
   static constexpr int KB = DP / 32;
   static constexpr int NB = DP / 16;
-  static constexpr int LB = DP * BITS / 32;
+  static constexpr int RPS = 16 / SLOTS;  // query rows (columns) per slot
+  static constexpr int LB = DP * BITS / 32;  // payload bytes per lane and side
   static constexpr int LW = LB / 4;
   static constexpr int CS = LB < 16 ? LB : 16;
   static constexpr int NCH = LB / CS;
-  static constexpr int MW = QUANT ? 4 * NG : 1;  // meta dwords per lane (4 tokens x NG)
-  // LDS ring slot of one tile: [K payload][V payload][K meta][V meta]
-  static constexpr int KP = LB * 64;
-  static constexpr int META = QUANT ? 128 * NG : 0;
-  static constexpr int SLOT = 2 * KP + META;
-  // tiles per wave ring (NBUF - 1 in flight): about 13 KB of LDS per wave, so
-  // three 4-wave workgroups fit a CU's 160 KB
-  static constexpr int NBUF_RAW = 13312 / SLOT;
-  static constexpr int NBUF = NBUF_RAW < 2 ? 2 : NBUF_RAW > 8 ? 8 : NBUF_RAW;
-  // LDS-DMA instructions per tile (each decrements vmcnt once)
-  static constexpr int PAY_INSTS = CS == 16 ? NCH : 2;
-  static constexpr int META_INSTS = QUANT ? (32 * NG + 63) / 64 : 0;
-  static constexpr int LPT = 2 * PAY_INSTS + META_INSTS;
-  static_assert((NBUF - 1) * LPT <= 63, "vmcnt range");
+  static constexpr int MW = QUANT ? 4 * NG : 4;  // meta dwords per lane (4 tokens x NG)
+  static_assert(SLOTS == 1 || RB == 1, "column slots need a single row block");
+  static_assert(CS == 16 || (CS == 8 && NCH == 1), "payload chunk");
 };
 
+// A lane's K or V payload of one tile, straight from HBM.
 template <typename C>
-struct Tile {
-  uint32_t k[C::LW];
-  uint32_t v[C::LW];
-  uint32_t km[C::MW];
-  uint32_t vm[C::MW];
-};
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Global -> LDS DMA of one 16- or 4-byte piece per lane: lane l's data lands
-// at dst + l*size (dst is wave-uniform).
-__device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void *src, uint8_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 4, 0, 0);
-}
-
-// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= VM only.
-template <int VM>
-__device__ __forceinline__ void wait_vm() {
-  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// Wait until the tile that has `younger` tiles issued after it has landed
-// (DMA groups complete in issue order).
-template <typename C, int K>
-__device__ __forceinline__ void wait_tile_rec(int younger) {
-  if constexpr (K == 0) {
-    wait_vm<0>();
-  } else {
-    if (younger >= K) wait_vm<K * C::LPT>();
-    else wait_tile_rec<C, K - 1>(younger);
-  }
-}
-template <typename C>
-__device__ __forceinline__ void wait_tile(int younger) {
-  wait_tile_rec<C, C::NBUF - 1>(younger);
-}
-
-// Issue the LDS-DMA of one 16-token tile (payload chunks + metadata words).
-template <typename C>
-__device__ __forceinline__ void issue_tile(uint8_t *slot, const AttnArgs &a, const uint8_t *head,
-                                           int tile_in_page, int lane) {
-  const int64_t off = (int64_t)tile_in_page * a.g.tile_bytes;
-  const uint8_t *kt = head + off, *vt = head + a.g.v_offset + off;
-  if constexpr (C::CS == 16) {
-#pragma unroll
-    for (int c = 0; c < C::NCH; ++c) dma16(kt + c * 1024 + lane * 16, slot + c * 1024);
-#pragma unroll
-    for (int c = 0; c < C::NCH; ++c) dma16(vt + c * 1024 + lane * 16, slot + C::KP + c * 1024);
-  } else {
-    dma4(kt + lane * 8, slot);
-    dma4(kt + lane * 8 + 4, slot + 256);
-    dma4(vt + lane * 8, slot + C::KP);
-    dma4(vt + lane * 8 + 4, slot + C::KP + 256);
-  }
-  if constexpr (C::QUANT) {
-    const int base = tile_in_page * PKV_TILE * C::NG;
-#pragma unroll
-    for (int m = 0; m < 32 * C::NG; m += 64) {
-      const int idx = m + lane;
-      if (idx < 32 * C::NG) {
-        const uint8_t *src = idx < 16 * C::NG
-                                 ? head + a.g.kmeta_offset + (int64_t)(base + idx) * 4
-                                 : head + a.g.vmeta_offset + (int64_t)(base + idx - 16 * C::NG) * 4;
-        dma4(src, slot + 2 * C::KP + m * 4);
-      }
-    }
-  }
-}
-
-// Registers of one tile from its LDS slot: lane payload and the lane's 4 tokens' meta.
-template <typename C>
-__device__ __forceinline__ void read_tile(Tile<C> &t, const uint8_t *slot, int lane, int jj) {
+__device__ __forceinline__ void load_payload(uint32_t (&w)[C::LW], const uint8_t *tile, int lane) {
   if constexpr (C::CS == 16) {
 #pragma unroll
     for (int c = 0; c < C::NCH; ++c) {
-      const u4 x = *(const u4 *)(slot + c * 1024 + lane * 16);
-      const u4 y = *(const u4 *)(slot + C::KP + c * 1024 + lane * 16);
-      t.k[4 * c] = x.x; t.k[4 * c + 1] = x.y; t.k[4 * c + 2] = x.z; t.k[4 * c + 3] = x.w;
-      t.v[4 * c] = y.x; t.v[4 * c + 1] = y.y; t.v[4 * c + 2] = y.z; t.v[4 * c + 3] = y.w;
+      const u4 x = *(const u4 *)(tile + c * 1024 + lane * 16);
+      w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
     }
   } else {
-    t.k[0] = *(const uint32_t *)(slot + lane * 4);
-    t.k[1] = *(const uint32_t *)(slot + 256 + lane * 4);
-    t.v[0] = *(const uint32_t *)(slot + C::KP + lane * 4);
-    t.v[1] = *(const uint32_t *)(slot + C::KP + 256 + lane * 4);
+    const u2 x = *(const u2 *)(tile + lane * 8);
+    w[0] = x.x; w[1] = x.y;
   }
-  if constexpr (C::QUANT) {
-    const uint32_t *km = (const uint32_t *)(slot + 2 * C::KP) + 4 * jj * C::NG;
-    const uint32_t *vm = km + 16 * C::NG;
+}
+
+// The metadata words (all groups) of a lane's four tokens: 4*NG contiguous dwords.
+template <typename C>
+__device__ __forceinline__ void load_meta(uint32_t (&mw)[C::MW], const uint8_t *p) {
 #pragma unroll
-    for (int i = 0; i < C::MW; i += 4) {
-      const u4 x = *(const u4 *)(km + i);
-      const u4 y = *(const u4 *)(vm + i);
-      t.km[i] = x.x; t.km[i + 1] = x.y; t.km[i + 2] = x.z; t.km[i + 3] = x.w;
-      t.vm[i] = y.x; t.vm[i + 1] = y.y; t.vm[i + 2] = y.z; t.vm[i + 3] = y.w;
-    }
+  for (int i = 0; i < C::MW; i += 4) {
+    const u4 x = *(const u4 *)(p + i * 4);
+    mw[i] = x.x; mw[i + 1] = x.y; mw[i + 2] = x.z; mw[i + 3] = x.w;
   }
 }
 
@@ -211,7 +172,7 @@ template <int FK>
 struct FloatOps;
 
 template <>
-struct FloatOps<1> {  // f16 pages
+struct FloatOps<1> {  // f16 operands (f16 pages, and codes of quantized pages)
   typedef h8 KT;
   typedef h4 VT;
   static __device__ __forceinline__ f4 qk(h8 a, h8 b, f4 c) {
@@ -223,7 +184,6 @@ struct FloatOps<1> {  // f16 pages
   static __device__ __forceinline__ h4 pack_p(float p0, float p1, float p2, float p3) {
     return h4{(_Float16)p0, (_Float16)p1, (_Float16)p2, (_Float16)p3};
   }
-  static __device__ __forceinline__ uint16_t from_float(float x) { return f32_to_f16_bits(x); }
 };
 
 template <>
@@ -240,182 +200,520 @@ struct FloatOps<0> {  // bf16 pages
     return s4{(short)f32_to_bf16_bits(p0), (short)f32_to_bf16_bits(p1),
               (short)f32_to_bf16_bits(p2), (short)f32_to_bf16_bits(p3)};
   }
-  static __device__ __forceinline__ uint16_t from_float(float x) { return f32_to_bf16_bits(x); }
 };
 
-template <int BITS, int DP, int G, int RB, int FK>
-__global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
-  using C = Cfg<BITS, DP, G, RB, FK>;
+
+// Tiles of a sequence: at least one, so that an empty sequence still owns a
+// piece that writes its zero output.
+__device__ __forceinline__ int seq_tiles(int len) {
+  return len <= 0 ? 1 : (len + PKV_TILE - 1) / PKV_TILE;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Work split.  Tiles are numbered over (sequence b, KV head kh, tile t) in
+// that order, T in all; the tiles of one (b, kh) form a segment.  Wave w of W
+// (W <= T) owns the run [start(w), start(w+1)): equal runs whatever the
+// lengths, so no wave waits on a ragged tail and each pays its start-up once.
+// A run is cut into pieces at segment boundaries.
+struct Split {
+  int T, W, q, r;  // T tiles over W waves: the first r runs have q + 1 tiles, the rest q
+  __device__ __forceinline__ void init(int t, int w) {
+    T = t; W = w; q = t / w; r = t - q * w;
+  }
+  __device__ __forceinline__ int start(int w) const { return w * q + min(w, r); }
+  // the wave whose run holds tile g
+  __device__ __forceinline__ int wave_of(int g) const {
+    const int big = r * (q + 1);
+    return g < big ? g / (q + 1) : r + (g - big) / q;
+  }
+};
+
+// Partial slots: the first piece of wave w's run goes to slot 2w, a later
+// (its last) one to 2w+1; pieces in between cover whole segments and write
+// the output directly.  The pieces of segment [s0, s1) are those of waves
+// wa .. wa+n-1; wave wa's piece is its first one unless its run started
+// before s0.
+struct SegPieces {
+  int n, wa, slot0;
+  __device__ __forceinline__ int slot(int i) const { return i == 0 ? slot0 : 2 * (wa + i); }
+};
+
+__device__ __forceinline__ SegPieces seg_pieces(const Split &sp, int s0, int s1) {
+  SegPieces p;
+  p.wa = sp.wave_of(s0);
+  p.n = sp.wave_of(s1 - 1) - p.wa + 1;
+  p.slot0 = sp.start(p.wa) < s0 ? 2 * p.wa + 1 : 2 * p.wa;
+  return p;
+}
+
+// Total tiles of a launch (wave-uniform): hk * sum over sequences of seq_tiles.
+__device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int hk, int lane) {
+  int t = 0;
+  for (int c0 = 0; c0 < batch; c0 += 64) {
+    const int idx = c0 + lane;
+    t += wave_sum(idx < batch ? seq_tiles(lens[idx]) : 0);
+  }
+  return __builtin_amdgcn_readfirstlane(t) * hk;
+}
+
+// Log-sum-exp merge of partition partials (paged_attention.py:191-204, in
+// the exp2 domain): one wave per (segment, query row) of a segment split over
+// several waves' runs; whole segments were written by the attention kernel.
+// Lane k holds piece k's weight 2^(m_k - M) / S; the output row accumulates
+// over the pieces with the lanes striding its DP columns.
+template <int DP>
+__global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
+  constexpr int PER = DP / 64 > 0 ? DP / 64 : 1;  // output columns per lane
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (gw >= a.batch * a.hk * a.rows) return;
+  const int row = gw % a.rows, seg = gw / a.rows;
+  const int b = seg / a.hk, kh = seg % a.hk;
+  // tiles before sequence b, and the launch's split (as the attention kernel made it)
+  int pre = 0, tiles = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int idx = c0 + lane;
+    const int nt = idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0;
+    tiles += wave_sum(nt);
+    pre += wave_sum(idx < b ? nt : 0);
+  }
+  const int T = __builtin_amdgcn_readfirstlane(tiles) * a.hk;
+  const int ntb = seq_tiles(a.seq_lens[b]);
+  const int s0 = __builtin_amdgcn_readfirstlane(pre) * a.hk + kh * ntb;
+  Split sp;
+  sp.init(T, min(a.waves, T));
+  const SegPieces pc = seg_pieces(sp, s0, s0 + ntb);
+  if (pc.n < 2) return;
+
+  // M = max m, S = sum l 2^(m - M) over the pieces (lanes stride the pieces)
+  float mx = -INFINITY, sm = 0.0f;
+  for (int k0 = 0; k0 < pc.n; k0 += 64) {
+    const int k = k0 + lane;
+    if (k < pc.n) {
+      const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
+      if (ml.y > 0.0f) {  // a piece with no visible token holds l = 0
+        const float nm = fmaxf(mx, ml.x);
+        sm = sm * __builtin_amdgcn_exp2f(mx - nm) + ml.y * __builtin_amdgcn_exp2f(ml.x - nm);
+        mx = nm;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sm, o, 64);
+    const float nm = fmaxf(mx, om);
+    sm = nm == -INFINITY ? 0.0f
+                         : sm * __builtin_amdgcn_exp2f(mx - nm) + os * __builtin_amdgcn_exp2f(om - nm);
+    mx = nm;
+  }
+  const float inv = 1.0f / fmaxf(sm, 1e-20f);
+  float acc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc[i] = 0.0f;
+  for (int k0 = 0; k0 < pc.n; k0 += 64) {
+    // lane j: weight of piece k0 + j
+    float wl = 0.0f;
+    {
+      const int k = k0 + lane;
+      if (k < pc.n) {
+        const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
+        wl = ml.y > 0.0f ? __builtin_amdgcn_exp2f(ml.x - mx) * inv : 0.0f;
+      }
+    }
+    const int kn = min(64, pc.n - k0);
+#pragma unroll 8
+    for (int j = 0; j < kn; ++j) {
+      const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
+      const float *src = a.part_acc + ((int64_t)pc.slot(k0 + j) * a.rows + row) * DP + lane * PER;
+      if constexpr (PER == 4) {
+        const f4 x = *(const f4 *)src;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += wk * x[i];
+      } else if constexpr (PER == 2) {
+        const float2 x = *(const float2 *)src;
+        acc[0] += wk * x.x;
+        acc[1] += wk * x.y;
+      } else {
+        acc[0] += wk * src[0];
+      }
+    }
+  }
+  const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
+  uint16_t *o = a.out + (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane * PER + i;
+    if (d < a.dim) o[d] = float_to_bits(acc[i], a.float_kind);
+  }
+}
+
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
+__global__ __launch_bounds__(64)
+__attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS)))) void attn_kernel(
+    const AttnArgs a) {
+  using C = Cfg<BITS, DP, G, RB, FK, SLOTS>;
   constexpr bool QUANT = C::QUANT;
-  constexpr int NG = C::NG, KB = C::KB, NB = C::NB;
+  constexpr int NG = C::NG, KB = C::KB, NB = C::NB, RPS = C::RPS;
   // MFMA operand types: quantized pages run in f16 (codes as 1024 + c).
   using FO = FloatOps<QUANT ? 1 : FK>;
   using KT = typename FO::KT;
   using VT = typename FO::VT;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15, jj = lane >> 4;
-  const int w = blockIdx.x * 4 + wave;
-  if (w >= a.max_units) return;
+  // Lane-derived values are refreshed at every piece through an opaque copy
+  // of the lane id, so the compiler recomputes per-lane addresses inside the
+  // piece loop instead of hoisting them all and pinning them in registers.
+  int lane = threadIdx.x;
+  int col, jj, slot_l, rowc;  // slot_l: this lane's column slot; rowc: its row within the slot
+  auto refresh_lane = [&]() __attribute__((always_inline)) {
+    asm volatile("" : "+v"(lane));
+    col = lane & 15;
+    jj = lane >> 4;
+    slot_l = col / RPS;
+    rowc = col % RPS;
+  };
+  refresh_lane();
+  const int w = blockIdx.x;
   const Geo &g = a.g;
-  const int kh = w % g.hk, su = w / g.hk;
-  int b, part, nsplit, first_unit;
-  if (!locate_unit(a.seq_lens, a.batch, a.split, su, lane, b, part, nsplit, first_unit)) return;
-  // wave-uniform values live in SGPRs: scalar branches, scalar loads
-  b = __builtin_amdgcn_readfirstlane(b);
-  part = __builtin_amdgcn_readfirstlane(part);
-  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
-  const int L = a.seq_lens[b];
-  const int t0 = part * a.split;
-  const int t1 = min(L, t0 + a.split);
-  const int width = a.widths ? a.widths[b] : a.nq;
-
-  // ---- query rows: row = rb*16 + col -> (q = row / gqa, h = kh*gqa + row % gqa)
-  int lim[RB];
-  KT qop[RB][KB];
-  float qs[RB][NG];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int row = rb * 16 + col;
-    const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-    const bool live = row < a.rows && qi < width;
-    int qp = -1;
-    if (live) qp = a.q_pos ? a.q_pos[(int64_t)b * a.nq + qi] : L - width + qi;
-    lim[rb] = live ? min(qp, t1 - 1) : -1;
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) qs[rb][gi] = 0.0f;
-    const uint16_t *qrow = a.q + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int d0 = 32 * kb + 8 * jj;
-      uint16_t raw[8];
-      if (row < a.rows && (g.dim & 7) == 0 && d0 + 8 <= g.dim) {
-        u4 x = *(const u4 *)(qrow + d0);
-        raw[0] = x.x & 0xFFFF; raw[1] = x.x >> 16; raw[2] = x.y & 0xFFFF; raw[3] = x.y >> 16;
-        raw[4] = x.z & 0xFFFF; raw[5] = x.z >> 16; raw[6] = x.w & 0xFFFF; raw[7] = x.w >> 16;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) raw[e] = (row < a.rows && d0 + e < g.dim) ? qrow[d0 + e] : 0;
-      }
-      if constexpr (QUANT || FK == 1) {
-        h8 v;
-        float sum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const _Float16 hv = (_Float16)bits_to_float(raw[e], g.float_kind);
-          v[e] = hv;
-          sum += (float)hv;
-        }
-        if constexpr (QUANT) qs[rb][(32 * kb) / G] += sum;
-        if constexpr (FK == 1 || QUANT) qop[rb][kb] = __builtin_bit_cast(KT, v);
-      } else {
-        u4 packed = {(uint32_t)raw[0] | ((uint32_t)raw[1] << 16), (uint32_t)raw[2] | ((uint32_t)raw[3] << 16),
-                     (uint32_t)raw[4] | ((uint32_t)raw[5] << 16), (uint32_t)raw[6] | ((uint32_t)raw[7] << 16)};
-        qop[rb][kb] = __builtin_bit_cast(KT, packed);
-      }
-    }
-    if constexpr (QUANT) {
-#pragma unroll
-      for (int gi = 0; gi < NG; ++gi) {
-        qs[rb][gi] += __shfl_xor(qs[rb][gi], 16, 64);
-        qs[rb][gi] += __shfl_xor(qs[rb][gi], 32, 64);
-      }
-    }
-  }
-
-  // ---- state
-  float m[RB], lsum[RB], corr[RB][NG];
-  f4 O[RB][NB], ones_acc[RB][NG];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    m[rb] = -INFINITY;
-    lsum[rb] = 0.0f;
-#pragma unroll
-    for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] = 0.0f; ones_acc[rb][gi] = f4{0, 0, 0, 0}; }
-  }
-
-  // page ids of this partition (split <= 64 pages)
-  const int first_page = t0 / g.page;
-  const int npages = t1 > t0 ? (t1 - 1) / g.page - first_page + 1 : 0;
-  int pid = 0;
-  if (lane < npages && first_page + lane < a.max_pages) {
-    pid = a.table[(int64_t)b * a.max_pages + first_page + lane];
-    if (pid < 0 || pid >= a.num_pages) pid = -1;
-  } else if (lane < npages) {
-    pid = -1;
-  }
-  // partitions start on page boundaries: tile -> (page, tile in page) by shifts
+  const int hk = g.hk;
   const int tpp_shift = __builtin_ctz(g.page / PKV_TILE);
-  const int ntiles = t1 > t0 ? (t1 - t0 + PKV_TILE - 1) / PKV_TILE : 0;
+  const int tpp_mask = (1 << tpp_shift) - 1;
 
-  auto head_of = [&](int tile, int &tip) -> const uint8_t * {
-    tip = tile & ((1 << tpp_shift) - 1);
-    const int id = __builtin_amdgcn_readlane(pid, tile >> tpp_shift);
-    if (id < 0) return nullptr;
-    return a.pool + (int64_t)id * g.page_bytes + (int64_t)kh * g.head_bytes;
+  // ---- sequences: lanes hold one 64-sequence chunk (length, tiles, inclusive
+  // tile prefix over all sequences); chunk_pre / chunk_end bound its prefix
+  int cbase = 0, len_l = 0, nt_l = 0, incl_l = 0, chunk_pre = 0, chunk_end = 0;
+  auto load_chunk = [&](int base, int pre) __attribute__((always_inline)) {
+    cbase = base;
+    chunk_pre = pre;
+    const int idx = base + lane;
+    len_l = idx < a.batch ? a.seq_lens[idx] : 0;
+    nt_l = idx < a.batch ? seq_tiles(len_l) : 0;
+    incl_l = wave_scan_incl(nt_l, lane) + pre;
+    chunk_end = __builtin_amdgcn_readlane(incl_l, 63);
+  };
+  load_chunk(0, 0);
+  int all_tiles = chunk_end;
+  for (int c0 = 64; c0 < a.batch; c0 += 64) {
+    const int idx = c0 + lane;
+    all_tiles += wave_sum(idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0);
+  }
+  // tile counts fit in int32: the host bounds batch * max_pages * pages' tiles * HK
+  const int T = __builtin_amdgcn_readfirstlane(all_tiles) * hk;
+  const int W = min(a.waves, T);
+  if (w >= W) return;
+  Split sp;
+  sp.init(T, W);
+
+  // the segment holding tile g (uniform): sequence, KV head, length, tiles, first tile
+  auto locate = [&](int gt, int &pb, int &pkh, int &pL, int &pnt, int &pseg0)
+      __attribute__((always_inline)) {
+    if (gt < chunk_pre * hk) load_chunk(0, 0);
+    while (gt >= chunk_end * hk && cbase + 64 < a.batch) load_chunk(cbase + 64, chunk_end);
+    const unsigned long long hit = __ballot(cbase + lane < a.batch && incl_l * hk > gt);
+    const int f = hit ? __ffsll((long long)hit) - 1 : 0;
+    pb = cbase + f;
+    pnt = __builtin_amdgcn_readlane(nt_l, f);
+    pL = __builtin_amdgcn_readlane(len_l, f);
+    const int pre = (__builtin_amdgcn_readlane(incl_l, f) - pnt) * hk;
+    pkh = (gt - pre) / pnt;
+    pseg0 = pre + pkh * pnt;
   };
 
-  const h4 ones = h4{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+  // ---- per-piece metadata, requested a piece ahead: page-id window (page
+  // win + lane), raw query words and query positions
+  auto fetch_window = [&](int pb, int win, int t1) __attribute__((always_inline)) -> int {
+    const int p = win + lane;
+    int id = -1;
+    if (p < a.max_pages && (int64_t)p * g.page < t1) id = a.table[(int64_t)pb * a.max_pages + p];
+    return id < a.num_pages ? id : -1;
+  };
+  auto fetch_q = [&](int pb, int pkh, u4 (&raw)[RB][KB], int (&qp)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = SLOTS > 1 ? rowc : rb * 16 + col;
+      const int rowv = row < a.rows ? row : 0;  // rows past the block load row 0, zeroed later
+      const int qi = rowv / a.gqa, h = pkh * a.gqa + rowv % a.gqa;
+      const uint16_t *qrow = a.q + (((int64_t)pb * a.heads + h) * a.nq + qi) * g.dim;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int d0 = 32 * kb + 8 * jj;
+        if ((g.dim & 7) == 0) {
+          raw[rb][kb] = *(const u4 *)(qrow + (d0 < g.dim ? d0 : 0));
+        } else {
+          uint16_t e8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) e8[e] = qrow[d0 + e < g.dim ? d0 + e : 0];
+          raw[rb][kb] = u4{(uint32_t)e8[0] | ((uint32_t)e8[1] << 16), (uint32_t)e8[2] | ((uint32_t)e8[3] << 16),
+                           (uint32_t)e8[4] | ((uint32_t)e8[5] << 16), (uint32_t)e8[6] | ((uint32_t)e8[7] << 16)};
+        }
+      }
+      qp[rb] = a.q_pos ? a.q_pos[(int64_t)pb * a.nq + qi] : 0;
+    }
+  };
 
-  // Tile body; `cur` holds the tile's payload and metadata registers.
-  auto process = [&](const Tile<C> &cur, int tile) __attribute__((always_inline)) {
+  // query operands and row limits of the current piece
+  int lim[RB];
+  KT qv[RB][KB];
+  float qs[RB][NG];
+  auto set_queries = [&](int pL, int pwidth, int t1, const u4 (&raw)[RB][KB], const int (&qp)[RB])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = SLOTS > 1 ? rowc : rb * 16 + col;
+      const bool valid = row < a.rows;
+      const int qi = row / a.gqa;
+      const bool live = valid && qi < pwidth;
+      const int pos = a.q_pos ? qp[rb] : pL - pwidth + qi;
+      lim[rb] = live ? min(pos, t1 - 1) : -1;
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) qs[rb][gi] = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int d0 = 32 * kb + 8 * jj;
+        u4 x = raw[rb][kb];
+        uint16_t e8[8] = {(uint16_t)(x.x & 0xFFFF), (uint16_t)(x.x >> 16), (uint16_t)(x.y & 0xFFFF),
+                          (uint16_t)(x.y >> 16), (uint16_t)(x.z & 0xFFFF), (uint16_t)(x.z >> 16),
+                          (uint16_t)(x.w & 0xFFFF), (uint16_t)(x.w >> 16)};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (!valid || d0 + e >= g.dim) e8[e] = 0;
+        if constexpr (QUANT || FK == 1) {
+          h8 v;
+          float sum = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const _Float16 hv = (_Float16)bits_to_float(e8[e], g.float_kind);
+            v[e] = hv;
+            sum += (float)hv;
+          }
+          if constexpr (QUANT) qs[rb][(32 * kb) / G] += sum;
+          qv[rb][kb] = __builtin_bit_cast(KT, v);
+        } else {
+          u4 packed = {(uint32_t)e8[0] | ((uint32_t)e8[1] << 16), (uint32_t)e8[2] | ((uint32_t)e8[3] << 16),
+                       (uint32_t)e8[4] | ((uint32_t)e8[5] << 16), (uint32_t)e8[6] | ((uint32_t)e8[7] << 16)};
+          qv[rb][kb] = __builtin_bit_cast(KT, packed);
+        }
+      }
+      if constexpr (QUANT) {
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          qs[rb][gi] += __shfl_xor(qs[rb][gi], 16, 64);
+          qs[rb][gi] += __shfl_xor(qs[rb][gi], 32, 64);
+        }
+      }
+    }
+  };
+  // slot j's query operand: the lane's rows in slot j's columns, zero elsewhere
+  auto qop = [&](int j, int rb, int kb) __attribute__((always_inline)) -> KT {
+    if constexpr (SLOTS == 1) return qv[rb][kb];
+    const u4 zero = {0, 0, 0, 0};
+    return slot_l == j ? qv[rb][kb] : __builtin_bit_cast(KT, zero);
+  };
+
+  // Tiles of iteration `it` of a piece (first tile pta, ntl tiles, page window
+  // pwin held in ppid): per slot, the byte offset of its head block in the pool
+  // and its tile within the page (uniform); bit j of the returned mask is set
+  // when slot j's tile exists.  Loads of absent tiles (past the piece, unmapped
+  // pages) read head block kh of page 0; their results are never used.
+  auto plan = [&](int pta, int ntl, int pwin, int ppid, int it, int (&pg)[SLOTS], int (&tp)[SLOTS])
+      __attribute__((always_inline)) {
+    int mask = 0;
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int tile = it * SLOTS + j;
+      int id = 0, t = 0;
+      if (tile < ntl) {
+        const int st = pta + tile;
+        const int pid_j = __builtin_amdgcn_readlane(ppid, (st >> tpp_shift) - pwin);
+        if (pid_j >= 0) {
+          id = pid_j;
+          t = st & tpp_mask;
+          mask |= 1 << j;
+        }
+      }
+      pg[j] = id;
+      tp[j] = t;
+    }
+    return mask;
+  };
+  // a tile's K payload in the pool (V is g.v_offset further)
+  auto tile_at = [&](int pkh, int id, int t) __attribute__((always_inline)) {
+    return a.pool + (int64_t)id * g.page_bytes + (int64_t)pkh * g.head_bytes + (int64_t)t * g.tile_bytes;
+  };
+  // the lane's metadata words (its slot's tile of iteration `it`, tokens 4*jj..4*jj+3)
+  auto meta_at = [&](int pkh, int pta, int ntl, int pwin, int ppid, int it, int64_t side)
+      __attribute__((always_inline)) {
+    const int tile = it * SLOTS + slot_l;
+    const int st = pta + tile;
+    const int id = __shfl(ppid, ((st >> tpp_shift) - pwin) & 63, 64);
+    const bool ok = tile < ntl && id >= 0;
+    const int64_t h = (int64_t)pkh * g.head_bytes + (ok ? (int64_t)id * g.page_bytes : 0);
+    const int t = ok ? st & tpp_mask : 0;
+    return a.pool + h + side + (int64_t)(t * PKV_TILE + 4 * jj) * (NG * 4);
+  };
+
+  uint32_t kw[SLOTS][C::LW], vw[SLOTS][C::LW];
+  uint32_t km[C::MW], vm[C::MW];
+  auto load_k = [&](int pkh, const int (&pg)[SLOTS], const int (&tp)[SLOTS], const uint8_t *mp)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) load_payload<C>(kw[j], tile_at(pkh, pg[j], tp[j]), lane);
+    if constexpr (QUANT) load_meta<C>(km, mp);
+  };
+  auto load_v = [&](int pkh, const int (&pg)[SLOTS], const int (&tp)[SLOTS], const uint8_t *mp)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) load_payload<C>(vw[j], tile_at(pkh, pg[j], tp[j]) + g.v_offset, lane);
+    if constexpr (QUANT) load_meta<C>(vm, mp);
+  };
+
+  // ---- pieces.  Current: tiles [cta, ctb) of segment (cb, ckh) starting at
+  // tile cseg0; the run ends at run_end.  Next (n*): the rest of the run.
+  const int run_end = sp.start(w + 1);
+  int cb, ckh, cL, cnt, cseg0;
+  bool cfirst = true;
+  locate(sp.start(w), cb, ckh, cL, cnt, cseg0);
+  int cta = sp.start(w) - cseg0;
+  int ctb = min(cnt, run_end - cseg0);
+  int cpid = fetch_window(cb, cta >> tpp_shift, min(cL, ctb * PKV_TILE));
+
+  bool has_next = false;
+  int nb = 0, nkh = 0, nL = 0, nnt = 1, nta = 0, ntb = 0, npid = -1, nseg0 = 0;
+
+  // next piece: the next segment's tiles up to the run's end, and its
+  // page-id window (read at the next switch)
+  auto set_next = [&](int gstart) __attribute__((always_inline)) {
+    locate(gstart, nb, nkh, nL, nnt, nseg0);
+    nta = gstart - nseg0;
+    ntb = min(nnt, run_end - nseg0);
+    npid = fetch_window(nb, nta >> tpp_shift, min(nL, ntb * PKV_TILE));
+  };
+
+  int pg[SLOTS], npg[SLOTS], tp[SLOTS], ntp[SLOTS];
+
+  for (;;) {
+    refresh_lane();
+    // ---- start the piece: query rows and its first tiles, in flight together
+    const int width = a.widths ? a.widths[cb] : a.nq;
+    const int t0 = cta * PKV_TILE;
+    const int t1 = min(cL, ctb * PKV_TILE);
+    const int ntl = t1 > t0 ? (t1 - t0 + PKV_TILE - 1) / PKV_TILE : 0;
+    const int niters = max(1, (ntl + SLOTS - 1) / SLOTS);
+    int cwin = cta >> tpp_shift;
+    int cmask;
     {
-      const int tok0 = t0 + tile * PKV_TILE;
-      // ---- S^T = K.Q^T
+      u4 raw[RB][KB];
+      int qp[RB];
+      fetch_q(cb, ckh, raw, qp);
+      cmask = plan(cta, ntl, cwin, cpid, 0, pg, tp);
+      load_k(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.kmeta_offset));
+      load_v(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.vmeta_offset));
+      set_queries(cL, width, t1, raw, qp);
+      // the rest of the run is the next piece: its page-id window now
+      has_next = cseg0 + ctb < run_end;
+      if (has_next) set_next(cseg0 + ctb);
+    }
+
+    float m[RB], lsum[RB], corr[RB][NG], osum[RB][NG];
+    f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      m[rb] = -INFINITY;
+      lsum[rb] = 0.0f;
+#pragma unroll
+      for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] = 0.0f; osum[rb][gi] = 0.0f; }
+    }
+
+    // One iteration over SLOTS tiles; with `more`, the next iteration's tiles
+    // are requested as soon as each half's registers are free (the last
+    // iteration is peeled so nothing is in flight across the epilogue).
+    auto iterate = [&](auto more, int it) __attribute__((always_inline)) {
+      constexpr bool MORE = decltype(more)::value;
+      refresh_lane();
+      if constexpr (SLOTS > 1) {
+        // Keep the per-slot query selects inside the loop: hoisted, they would
+        // pin SLOTS masked copies of Q in VGPRs for the whole piece.
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) asm volatile("" : "+v"(qv[rb][kb]));
+      }
+      // S^T for the iteration's tiles (slot j -> columns of slot j)
       f4 acc[RB][NG];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) acc[rb][gi] = f4{0, 0, 0, 0};
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        KT kop;
-        if constexpr (QUANT) {
-          kop = Conv<BITS>::template kop<C::LW>(cur.k, kb);
-        } else {
-          u4 r = {cur.k[4 * kb], cur.k[4 * kb + 1], cur.k[4 * kb + 2], cur.k[4 * kb + 3]};
-          kop = __builtin_bit_cast(KT, r);
-        }
-        const int gi = QUANT ? (32 * kb) / G : 0;
+      for (int j = 0; j < SLOTS; ++j) {
+        if (cmask & (1 << j)) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[rb][gi] = FO::qk(kop, qop[rb][kb], acc[rb][gi]);
-      }
-      // ---- scores (exp2 domain)
-      float s[RB][4];
-      float ksf[4][NG], kbf[4][NG];
-      if constexpr (QUANT) {
+          for (int kb = 0; kb < KB; ++kb) {
+            KT kop;
+            if constexpr (QUANT) {
+              kop = Conv<BITS>::template kop<C::LW>(kw[j], kb);
+            } else {
+              u4 r = {kw[j][4 * kb], kw[j][4 * kb + 1], kw[j][4 * kb + 2], kw[j][4 * kb + 3]};
+              kop = __builtin_bit_cast(KT, r);
+            }
+            const int gi = QUANT ? (32 * kb) / G : 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int gi = 0; gi < NG; ++gi) {
-            const uint32_t word = cur.km[r * NG + gi];
-            ksf[r][gi] = f16_bits_to_f32(word);
-            kbf[r][gi] = f16_bits_to_f32(word >> 16) - 1024.0f * ksf[r][gi];
+            for (int rb = 0; rb < RB; ++rb) acc[rb][gi] = FO::qk(kop, qop(j, rb, kb), acc[rb][gi]);
           }
+        }
       }
+      // scores of the lane's tile (its slot's tile of this iteration)
+      const bool my_ok = (cmask >> slot_l) & 1;
+      const int tok0 = t0 + (it * SLOTS + slot_l) * PKV_TILE + 4 * jj;
+      float s[RB][4];
+      bool vis[RB][4];
       bool need = false;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float v;
           if constexpr (QUANT) {
             v = 0.0f;
 #pragma unroll
-            for (int gi = 0; gi < NG; ++gi) v += ksf[r][gi] * acc[rb][gi][r] + qs[rb][gi] * kbf[r][gi];
+            for (int gi = 0; gi < NG; ++gi) {
+              const uint32_t word = km[r * NG + gi];
+              const float ks = f16_bits_to_f32(word);
+              const float kbias = f16_bits_to_f32(word >> 16) - 1024.0f * ks;
+              v += ks * acc[rb][gi][r] + qs[rb][gi] * kbias;
+            }
           } else {
             v = acc[rb][0][r];
           }
-          const int t = tok0 + 4 * jj + r;
-          v = t <= lim[rb] ? v * a.scale_log2 : -INFINITY;
+          vis[rb][r] = my_ok && tok0 + r <= lim[rb];
+          v = vis[rb][r] ? v * a.scale_log2 : -INFINITY;
           s[rb][r] = v;
           need |= v > m[rb] + kTau;
         }
+      // K registers and score metadata are free: request the next iteration's
+      int nmask = 0;
+      const uint8_t *nmv = nullptr;
+      if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int first = cta + (it + 1) * SLOTS;
+        const int last = cta + min((it + 1) * SLOTS + SLOTS, ntl) - 1;
+        if ((last >> tpp_shift) - cwin > 63) {
+          cwin = first >> tpp_shift;  // the iteration's tiles leave the window: slide it
+          cpid = fetch_window(cb, cwin, t1);
+        }
+        nmask = plan(cta, ntl, cwin, cpid, it + 1, npg, ntp);
+        load_k(ckh, npg, ntp, meta_at(ckh, cta, ntl, cwin, cpid, it + 1, g.kmeta_offset));
+        nmv = meta_at(ckh, cta, ntl, cwin, cpid, it + 1, g.vmeta_offset);
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (__any(need)) {
+        // move a column's running max (column = same lane across jj)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           float tm = fmaxf(fmaxf(s[rb][0], s[rb][1]), fmaxf(s[rb][2], s[rb][3]));
@@ -426,265 +724,174 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
           m[rb] = mn;
           lsum[rb] *= alpha;
 #pragma unroll
-          for (int gi = 0; gi < NG; ++gi) corr[rb][gi] *= alpha;
+          for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] *= alpha; osum[rb][gi] *= alpha; }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float ar = __shfl(alpha, 4 * jj + r, 64);
-#pragma unroll
-            for (int n = 0; n < NB; ++n) O[rb][n][r] *= ar;
-#pragma unroll
-            for (int gi = 0; gi < NG; ++gi) ones_acc[rb][gi][r] *= ar;
-          }
+          for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
       }
-      // ---- probabilities and O += P'.V
-      float p[RB][4];
+      // probabilities and the P operands (per group for quantized V)
+      VT pop[RB][NG];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = tok0 + 4 * jj + r;
-          p[rb][r] = t <= lim[rb] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
-        }
-        lsum[rb] += (p[rb][0] + p[rb][1]) + (p[rb][2] + p[rb][3]);
-      }
-      if constexpr (QUANT) {
-        float vsf[4][NG], vbf[4][NG];
+        float p[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
+          p[r] = vis[rb][r] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
+        lsum[rb] += (p[0] + p[1]) + (p[2] + p[3]);
+        if constexpr (QUANT) {
 #pragma unroll
           for (int gi = 0; gi < NG; ++gi) {
-            const uint32_t word = cur.vm[r * NG + gi];
-            vsf[r][gi] = f16_bits_to_f32(word);
-            vbf[r][gi] = f16_bits_to_f32(word >> 16);
+            h4 pv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t word = vm[r * NG + gi];
+              // absent tokens contribute exact zeros whatever their metadata holds
+              const _Float16 ps = (_Float16)(p[r] * f16_bits_to_f32(word));
+              pv[r] = vis[rb][r] ? ps : (_Float16)0.0f;
+              corr[rb][gi] += vis[rb][r] ? p[r] * f16_bits_to_f32(word >> 16) : 0.0f;
+              osum[rb][gi] += (float)pv[r];
+            }
+            pop[rb][gi] = pv;
           }
-        h4 pv[RB][NG];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int gi = 0; gi < NG; ++gi) {
-            pv[rb][gi] = h4{(_Float16)(p[rb][0] * vsf[0][gi]), (_Float16)(p[rb][1] * vsf[1][gi]),
-                            (_Float16)(p[rb][2] * vsf[2][gi]), (_Float16)(p[rb][3] * vsf[3][gi])};
-            corr[rb][gi] += (p[rb][0] * vbf[0][gi] + p[rb][1] * vbf[1][gi]) +
-                            (p[rb][2] * vbf[2][gi] + p[rb][3] * vbf[3][gi]);
-          }
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-          const h4 vop = Conv<BITS>::template vop<C::LW>(cur.v, n);
-          const int gi = (16 * n) / G;
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) O[rb][n] = FO::pv(pv[rb][gi], vop, O[rb][n]);
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int gi = 0; gi < NG; ++gi) ones_acc[rb][gi] = FO::pv(pv[rb][gi], ones, ones_acc[rb][gi]);
-      } else {
-        VT pv[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) pv[rb] = FO::pack_p(p[rb][0], p[rb][1], p[rb][2], p[rb][3]);
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-          u2 r = {cur.v[2 * n], cur.v[2 * n + 1]};
-          const VT vop = __builtin_bit_cast(VT, r);
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) O[rb][n] = FO::pv(pv[rb], vop, O[rb][n]);
+        } else {
+          pop[rb][0] = FO::pack_p(p[0], p[1], p[2], p[3]);
         }
       }
-    }
-  };
+      // O^T += V^T . P'^T for each tile
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j) {
+        if (cmask & (1 << j)) {
+          VT bop[RB][NG];
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+              const u2 zero = {0, 0};
+              bop[rb][gi] = (SLOTS == 1 || slot_l == j) ? pop[rb][gi] : __builtin_bit_cast(VT, zero);
+            }
+#pragma unroll
+          for (int n = 0; n < NB; ++n) {
+            VT vop;
+            if constexpr (QUANT) {
+              vop = Conv<BITS>::template vop<C::LW>(vw[j], n);
+            } else {
+              u2 r = {vw[j][2 * n], vw[j][2 * n + 1]};
+              vop = __builtin_bit_cast(VT, r);
+            }
+            const int gi = QUANT ? (16 * n) / G : 0;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) O[rb][n] = FO::pv(vop, bop[rb][gi], O[rb][n]);
+          }
+        }
+      }
+      // V registers and value metadata are free: request the next iteration's
+      if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(ckh, npg, ntp, nmv);
+        __builtin_amdgcn_sched_barrier(0);
+        cmask = nmask;
+#pragma unroll
+        for (int j = 0; j < SLOTS; ++j) { pg[j] = npg[j]; tp[j] = ntp[j]; }
+      }
+    };
+    for (int it = 0; it + 1 < niters; ++it) iterate(std::true_type(), it);
+    iterate(std::false_type(), niters - 1);
 
-  // LDS ring of NBUF tile slots per wave, filled by DMA NBUF - 1 tiles ahead.
-  __shared__ __attribute__((aligned(16))) uint8_t ring[4][C::NBUF][C::SLOT];
-  uint8_t(*slots)[C::SLOT] = ring[wave];
-  int valid = 0;  // bit s: slot s holds a tile of a valid page
-  auto issue = [&](int tile) __attribute__((always_inline)) {
-    int tip;
-    const uint8_t *h = head_of(tile, tip);
-    const int s = tile % C::NBUF;
-    if (h) {
-      valid |= 1 << s;
-    } else {
-      // keep one DMA group per tile so vmcnt accounting stays exact
-      valid &= ~(1 << s);
-      h = a.pool + (int64_t)kh * g.head_bytes;
-      tip = 0;
-    }
-    issue_tile<C>(slots[s], a, h, tip, lane);
-  };
+    // ---- piece epilogue: fold the 4 jj lanes of a column, then the slots of a
+    // row, and write the output (whole segment) or the partial
+    const bool whole = cta == 0 && ctb == cnt;
+    const int slot = cfirst ? 2 * w : 2 * w + 1;
 #pragma unroll
-  for (int p = 0; p < C::NBUF - 1; ++p)
-    if (p < ntiles) issue(p);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    // refill the slot tile-1 used; its LDS reads have completed
-    wait_lgkm0();
-    __builtin_amdgcn_sched_barrier(0);
-    if (tile + C::NBUF - 1 < ntiles) issue(tile + C::NBUF - 1);
-    wait_tile<C>(min(ntiles - 1 - tile, C::NBUF - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    const int s = tile % C::NBUF;
-    if (valid & (1 << s)) {
-      Tile<C> cur;
-      read_tile<C>(cur, slots[s], lane, jj);
-      process(cur, tile);
-    }
-  }
-
-  // ---- epilogue: reduce l and the V-bias sums over the 4 token lanes of a row
+    for (int rb = 0; rb < RB; ++rb) {
+      lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
+      lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
-    lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
+      for (int gi = 0; gi < NG; ++gi) {
+        corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
+        corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
+        osum[rb][gi] += __shfl_xor(osum[rb][gi], 16, 64);
+        osum[rb][gi] += __shfl_xor(osum[rb][gi], 32, 64);
+      }
+      float mrow = m[rb], lrow = lsum[rb], wgt = 1.0f;
+      if constexpr (SLOTS > 1) {
+        // the row's slot columns (lanes col, col +- RPS, ...) merge by log-sum-exp
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-      corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
-      corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
-    }
-  }
-  const bool direct = nsplit == 1;
+        for (int o = RPS; o < 16; o <<= 1) mrow = fmaxf(mrow, __shfl_xor(mrow, o, 64));
+        wgt = lsum[rb] > 0.0f ? __builtin_amdgcn_exp2f(m[rb] - mrow) : 0.0f;
+        lrow = wgt * lsum[rb];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int src = 4 * jj + r;  // lane holding row (rb*16 + src) in the score layout
-      const float mr = __shfl(m[rb], src, 64);
-      const float lr = __shfl(lsum[rb], src, 64);
-      float cr[NG];
-#pragma unroll
-      for (int gi = 0; gi < NG; ++gi) cr[gi] = __shfl(corr[rb][gi], src, 64);
-      const int row = rb * 16 + src;
-      if (row >= a.rows) continue;
-      const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-      const float inv = 1.0f / fmaxf(lr, 1e-20f);
-      const int64_t obase = (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
-      const int64_t pbase = ((int64_t)w * a.rows + row) * DP;
+        for (int o = RPS; o < 16; o <<= 1) lrow += __shfl_xor(lrow, o, 64);
+      }
+      const int row = SLOTS > 1 ? rowc : rb * 16 + col;
+      const bool writer = slot_l == 0 && row < a.rows;
+      const int qi = row / a.gqa, h = ckh * a.gqa + row % a.gqa;
+      const float inv = 1.0f / fmaxf(lrow, 1e-20f);
+      uint16_t *o = a.out + (((int64_t)cb * a.heads + h) * a.nq + qi) * g.dim;
+      float *pa = a.part_acc + ((int64_t)slot * a.rows + row) * DP;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const int d = 16 * n + col;
-        float val = O[rb][n][r];
-        if constexpr (QUANT) {
-          const int gi = (16 * n) / G;
-          val += cr[gi] - 1024.0f * ones_acc[rb][gi][r];
+        float v4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = O[rb][n][r];
+          if constexpr (QUANT) {
+            const int gi = (16 * n) / G;
+            v += corr[rb][gi] - 1024.0f * osum[rb][gi];
+          }
+          v *= wgt;
+          if constexpr (SLOTS > 1) {
+#pragma unroll
+            for (int o2 = RPS; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+          }
+          v4[r] = v;
         }
-        if (direct) {
-          if (d < g.dim) a.out[obase + d] = float_to_bits(val * inv, g.float_kind);
+        if (!writer) continue;
+        const int d = 16 * n + 4 * jj;
+        if (whole) {
+          if ((g.dim & 3) == 0 && d + 4 <= g.dim) {
+            u2 packed = {(uint32_t)float_to_bits(v4[0] * inv, g.float_kind) |
+                             ((uint32_t)float_to_bits(v4[1] * inv, g.float_kind) << 16),
+                         (uint32_t)float_to_bits(v4[2] * inv, g.float_kind) |
+                             ((uint32_t)float_to_bits(v4[3] * inv, g.float_kind) << 16)};
+            *(u2 *)(o + d) = packed;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (d + r < g.dim) o[d + r] = float_to_bits(v4[r] * inv, g.float_kind);
+          }
         } else {
-          a.part_acc[pbase + d] = val;
+          *(f4 *)(pa + d) = f4{v4[0], v4[1], v4[2], v4[3]};
         }
       }
-      if (!direct && col == 0) {
-        a.part_ml[((int64_t)w * a.rows + row) * 2] = mr;
-        a.part_ml[((int64_t)w * a.rows + row) * 2 + 1] = lr;
-      }
+      if (writer && !whole && jj == 0)
+        *(float2 *)(a.part_ml + ((int64_t)slot * a.rows + row) * 2) = make_float2(mrow, lrow);
     }
-  }
-}
 
-// Log-sum-exp merge of partition partials (paged_attention.py:191-204, exp2
-// domain): one wave per (sequence, KV head).
+    // ---- switch to the next piece
+    if (!has_next) break;
+    cb = nb; ckh = nkh; cL = nL; cnt = nnt; cseg0 = nseg0; cta = nta; ctb = ntb;
+    cfirst = false; cpid = npid;
+  }
 
-__global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
-  // one wave per (sequence, KV head, query row)
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t w = (int64_t)blockIdx.x * 4 + wave;
-  if (w >= (int64_t)a.batch * a.hk * a.rows) return;
-  const int row = (int)(w % a.rows);
-  const int kh = (int)((w / a.rows) % a.hk);
-  const int b = (int)(w / ((int64_t)a.rows * a.hk));
-  const int nsplit = splits_of(a.seq_lens[b], a.split);
-  if (nsplit <= 1) return;
-  // first unit of sequence b: prefix sum of the partition counts
-  int carry = 0, first = 0;
-  for (int c0 = 0; c0 < a.batch; c0 += 64) {
-    const int idx = c0 + lane;
-    const int ns = idx < a.batch ? splits_of(a.seq_lens[idx], a.split) : 0;
-    const int incl = wave_scan_incl(ns, lane) + carry;
-    if (b >= c0 && b < c0 + 64) first = __shfl(incl - ns, b - c0, 64);
-    carry = __shfl(incl, 63, 64);
-  }
-  // partitions past the launched units were never computed: never read them
-  if (first + nsplit > a.max_units) return;
-  const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-  auto unit = [&](int s) { return ((int64_t)(first + s) * a.hk + kh) * a.rows + row; };
-  // global max over live partitions (lanes stride the partitions)
-  __shared__ float s_w[4][64];
-  float top = -INFINITY;
-  for (int s = lane; s < nsplit; s += 64) {
-    const float ms = a.part_ml[unit(s) * 2], ls = a.part_ml[unit(s) * 2 + 1];
-    if (ls > 0.0f) top = fmaxf(top, ms);
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) top = fmaxf(top, __shfl_xor(top, o, 64));
-  float norm = 0.0f;
-  float acc[4] = {0, 0, 0, 0};
-  const int per_lane = (a.dp + 63) / 64;
-  for (int s0 = 0; s0 < nsplit; s0 += 64) {
-    const int s = s0 + lane;
-    float wgt = 0.0f, ls = 0.0f;
-    if (s < nsplit) {
-      const float ms = a.part_ml[unit(s) * 2];
-      ls = a.part_ml[unit(s) * 2 + 1];
-      wgt = ls > 0.0f ? exp2f(ms - top) : 0.0f;  // dead partitions hold acc = 0
-    }
-    norm += wgt * ls;
-    s_w[wave][lane] = wgt;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int count = min(64, nsplit - s0);
-    // independent loads: each lane owns per_lane consecutive d of every partition
-    int j = 0;
-    for (; j + 4 <= count; j += 4) {
-      float v[4][4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float *pa = a.part_acc + unit(s0 + j + u) * a.dp;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[u][i] = i < per_lane ? pa[lane * per_lane + i] : 0.0f;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float wj = s_w[wave][j + u];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += wj * v[u][i];
-      }
-    }
-    for (; j < count; ++j) {
-      const float *pa = a.part_acc + unit(s0 + j) * a.dp;
-      const float wj = s_w[wave][j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i < per_lane) acc[i] += wj * pa[lane * per_lane + i];
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) norm += __shfl_xor(norm, o, 64);
-  const float inv = 1.0f / fmaxf(norm, 1e-20f);
-  const int64_t obase = (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = lane * per_lane + i;
-    if (i < per_lane && d < a.dim) a.out[obase + d] = float_to_bits(acc[i] * inv, a.float_kind);
-  }
 }
 
 // ---- host launcher ------------------------------------------------------------
 
-template <int BITS, int DP, int G, int RB, int FK>
-static hipError_t launch_one(hipStream_t stream, const AttnArgs &a) {
-  dim3 grid((unsigned)((a.max_units + 3) / 4)), block(256);
-  hipLaunchKernelGGL((attn_kernel<BITS, DP, G, RB, FK>), grid, block, 0, stream, a);
-  return hipGetLastError();
+typedef void (*AttnKernel)(AttnArgs);
+
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
+static AttnKernel kernel_of() {
+  if constexpr (RB > 1 && DP > 128) {
+    return nullptr;  // 17..32 rows at head_dim > 128: callers split the rows
+  } else {
+    return attn_kernel<BITS, DP, G, RB, FK, fit_slots(BITS, DP, G, SLOTS)>;
+  }
 }
 
-template <int RB>
-static hipError_t dispatch_rb(hipStream_t stream, const AttnArgs &a) {
-  const Geo &g = a.g;
-#define PKV_Q(BITS_, DP_, G_)                                                        \
-  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_)                               \
-    return launch_one<BITS_, DP_, G_, RB, 1>(stream, a);
+template <int RB, int SLOTS>
+static AttnKernel select_shape(const Geo &g) {
+#define PKV_Q(BITS_, DP_, G_) \
+  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return kernel_of<BITS_, DP_, G_, RB, 1, SLOTS>();
   PKV_Q(8, 64, 32) PKV_Q(8, 64, 64)
   PKV_Q(8, 128, 32) PKV_Q(8, 128, 64) PKV_Q(8, 128, 128)
   PKV_Q(8, 256, 32) PKV_Q(8, 256, 64) PKV_Q(8, 256, 128)
@@ -692,25 +899,49 @@ static hipError_t dispatch_rb(hipStream_t stream, const AttnArgs &a) {
   PKV_Q(4, 128, 32) PKV_Q(4, 128, 64) PKV_Q(4, 128, 128)
   PKV_Q(4, 256, 32) PKV_Q(4, 256, 64) PKV_Q(4, 256, 128)
 #undef PKV_Q
-#define PKV_F(DP_, FK_)                                                              \
-  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_)                            \
-    return launch_one<16, DP_, 32, RB, FK_>(stream, a);
+#define PKV_F(DP_, FK_) \
+  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_) return kernel_of<16, DP_, 32, RB, FK_, SLOTS>();
   PKV_F(64, 0) PKV_F(64, 1) PKV_F(128, 0) PKV_F(128, 1) PKV_F(256, 0) PKV_F(256, 1)
 #undef PKV_F
-  return hipErrorInvalidValue;
+  return nullptr;
 }
 
-hipError_t launch_attention(hipStream_t stream, const AttnArgs &a, int row_blocks) {
-  if (a.max_units <= 0) return hipSuccess;
-  if (row_blocks == 1) return dispatch_rb<1>(stream, a);
-  if (row_blocks == 2) return dispatch_rb<2>(stream, a);
-  return hipErrorInvalidValue;
+// Rows per KV head -> column slots: <= 4 rows: 4 slots, <= 8: 2, else 1
+// (two row blocks past 16 rows).
+static AttnKernel select_kernel(const Geo &g, int rows) {
+  if (rows <= 4) return select_shape<1, 4>(g);
+  if (rows <= 8) return select_shape<1, 2>(g);
+  if (rows <= 16) return select_shape<1, 1>(g);
+  if (rows <= 32) return select_shape<2, 1>(g);
+  return nullptr;
+}
+
+int attention_waves(const Geo &g, int rows) {
+  const AttnKernel k = select_kernel(g, rows);
+  if (!k) return -1;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64, 0) != hipSuccess) return -1;
+  return max(1, cus * per_cu);
+}
+
+hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
+  const AttnKernel k = select_kernel(a.g, a.rows);
+  if (!k) return hipErrorInvalidValue;
+  if (a.waves <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64), 0, stream, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a) {
   const int64_t waves = (int64_t)a.batch * a.hk * a.rows;
-  if (waves == 0) return hipSuccess;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, a);
+  if (waves == 0 || a.waves <= 1) return hipSuccess;  // one run covers every segment whole
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  if (a.dp == 64) hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, stream, a);
+  else if (a.dp == 128) hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, stream, a);
+  else if (a.dp == 256) hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, stream, a);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

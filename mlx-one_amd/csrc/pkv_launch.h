@@ -26,6 +26,10 @@ struct GatherArgs {
   int ngr;                 // reference groups per row
 };
 
+// Partial slots of the attention workspace per work wave: the first and the
+// last piece of its run.
+constexpr int kSlotsPerWave = 2;
+
 struct AttnArgs {
   Geo g;
   const uint8_t *pool;
@@ -36,16 +40,15 @@ struct AttnArgs {
   int max_pages;
   const int32_t *seq_lens, *q_pos, *widths;
   float scale_log2;  // softmax scale * log2(e)
-  int split;         // tokens per partition
-  int max_units;
-  float *part_acc;   // [units*HK][rows][DP]
-  float *part_ml;    // [units*HK][rows][2]
+  int waves;         // work waves (grid size)
+  float *part_acc;   // [2*waves][rows][DP]
+  float *part_ml;    // [2*waves][rows][2]
   uint16_t *out;     // [B][H][Q][D]
 };
 
 struct MergeArgs {
-  int batch, hk, heads, nq, gqa, rows, dim, dp, split, float_kind;
-  int max_units;  // launched (sequence, partition) units
+  int batch, hk, heads, nq, gqa, rows, dim, dp, float_kind;
+  int waves;  // as launched for the attention kernel
   const int32_t *seq_lens;
   const float *part_acc, *part_ml;
   uint16_t *out;
@@ -73,7 +76,10 @@ hipError_t launch_append(hipStream_t stream, const AppendArgs &a);
 hipError_t launch_gather(hipStream_t stream, const GatherArgs &a);
 hipError_t launch_copy(hipStream_t stream, uint8_t *pool, int64_t num_pages, int64_t page_bytes,
                        const int32_t *src, const int32_t *dst, int count);
-hipError_t launch_attention(hipStream_t stream, const AttnArgs &a, int row_blocks);
+hipError_t launch_attention(hipStream_t stream, const AttnArgs &a);
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a);
+// Resident waves of the attention kernel for this layout and row count on the
+// current device (CUs x workgroups per CU); <0 on error.
+int attention_waves(const Geo &g, int rows);
 
 }  // namespace pkv

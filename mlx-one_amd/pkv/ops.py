@@ -17,7 +17,6 @@ from pkv import _native as nat
 
 FLOAT_KINDS = {torch.bfloat16: 0, torch.float16: 1}
 DTYPES = {0: torch.bfloat16, 1: torch.float16}
-DEFAULT_SPLIT_TOKENS = 256
 MAX_ROWS = 32          # query rows (queries x heads per KV head) per attention launch
 
 
@@ -115,40 +114,42 @@ def append_quantize(fmt: PageFormat, pool, keys, values, block_table, start_pos,
     nat.check(code, "paged append")
 
 
-def plan_partitions(lengths, page_tokens, num_kv_heads=1, split_tokens=0, target_waves=4096):
-    """Partition size and unit count for host-known sequence lengths.
-
-    One wave of the attention kernel handles one (sequence, partition, KV
-    head).  ``split_tokens`` (a multiple of the page, 128..1024 tokens) is
-    chosen so that the launch has about ``target_waves`` waves -- enough to
-    keep every CU of the chip streaming -- and ``(split_tokens, units)`` is
-    returned with ``units = sum_b max(1, ceil(L_b / split))``.
-    """
-    lengths = [int(x) for x in lengths]
-    if split_tokens <= 0:
-        total = sum(max(x, 1) for x in lengths)
-        target_units = max(1, target_waves // max(num_kv_heads, 1))
-        split = max(DEFAULT_SPLIT_TOKENS // 2, min(1024, total // target_units))
-        split = max(page_tokens, (split + page_tokens - 1) // page_tokens * page_tokens)
-        split = min(split, 64 * page_tokens)
-        split_tokens = split
-    units = sum(max(1, math.ceil(x / split_tokens)) for x in lengths)
-    return split_tokens, units
+def attention_waves(fmt: PageFormat, num_heads, num_queries):
+    """Waves the attention kernel keeps resident for this shape (the default grid)."""
+    waves = int(nat.load().pkv_attention_waves(fmt.c_layout, num_heads, num_queries))
+    if waves <= 0:
+        nat.check(nat.PKV_LAUNCH_FAILED, "attention waves")
+    return waves
 
 
-def workspace_bytes(fmt: PageFormat, num_heads, num_queries, units):
+def workspace_bytes(fmt: PageFormat, num_heads, num_queries, waves):
     return int(nat.load().pkv_attention_workspace_bytes(fmt.c_layout, num_heads, num_queries,
-                                                          units))
+                                                          waves))
+
+
+# One attention workspace per device, grown on demand; calls on one stream
+# share it (each call's partials are merged before the next call starts).
+_WORKSPACES = {}
+
+
+def attention_workspace(device, nbytes):
+    """A workspace of at least ``nbytes`` on ``device`` (cached, grown on demand)."""
+    key = torch.device(device)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=key)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, scale, q_pos=None,
-                    widths=None, split_tokens=0, units=None, lengths_host=None, workspace=None,
-                    out=None):
+                    widths=None, waves=0, workspace=None, out=None):
     """Attention of ``queries [B, H, Q, D]`` over the paged cache.
 
     ``seq_lens`` counts the tokens in each sequence's cache (after the
-    append).  ``units`` / ``split_tokens`` may be given; otherwise they come
-    from ``lengths_host`` (host ints) or a copy of ``seq_lens`` to the host.
+    append) and stays on the device: the kernel shares the tiles of all
+    sequences out over ``waves`` waves (default: the resident capacity).
+    ``workspace`` (bytes from ``workspace_bytes``) may be given by the caller.
     """
     if queries.dim() != 4:
         raise ValueError("queries must be [B, H, Q, D]")
@@ -159,7 +160,6 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
         # wide query blocks (prefill) run as launches of <= MAX_ROWS rows per KV head
         device = queries.device
         lens = _i32(seq_lens, device)
-        host = lengths_host if lengths_host is not None else lens.cpu().tolist()
         pos = _i32(q_pos, device) if q_pos is not None else (
             lens[:, None] - (_i32(widths, device)[:, None] if widths is not None else nq)
             + torch.arange(nq, device=device, dtype=torch.int32)[None])
@@ -171,8 +171,8 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
             e = min(nq, s + per_launch)
             part = paged_attention(fmt, pool, queries[:, :, s:e].contiguous(), block_table, lens,
                                    scale=scale, q_pos=pos[:, s:e].contiguous(),
-                                   widths=(wid - s).clamp(0, e - s), split_tokens=split_tokens,
-                                   lengths_host=host, workspace=workspace)
+                                   widths=(wid - s).clamp(0, e - s), waves=waves,
+                                   workspace=workspace)
             out[:, :, s:e] = part
         return out
     if dim != fmt.head_dim:
@@ -181,13 +181,13 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     device = queries.device
     table = _i32(block_table, device)
     lens = _i32(seq_lens, device)
-    if units is None or split_tokens <= 0:
-        host = lengths_host if lengths_host is not None else lens.cpu().tolist()
-        split_tokens, units = plan_partitions(host, fmt.page_tokens, fmt.num_kv_heads,
-                                              split_tokens)
-    need = workspace_bytes(fmt, heads, nq, units)
-    if units > batch and (workspace is None or workspace.numel() < need):
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if waves <= 0:
+        waves = attention_waves(fmt, heads, nq)
+    need = workspace_bytes(fmt, heads, nq, waves)
+    if need < 0:
+        nat.check(nat.PKV_INVALID_ARGUMENT, "paged attention workspace")
+    if workspace is None:
+        workspace = attention_workspace(device, need)
     if out is None:
         out = torch.empty_like(queries)
     queries = queries.contiguous()
@@ -195,8 +195,7 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
         nat.stream_handle(device), fmt.c_layout, nat.ptr(pool), pool.shape[0], nat.ptr(queries),
         batch, heads, nq, nat.ptr(table), table.shape[1], nat.ptr(lens),
         nat.ptr(_i32(q_pos, device)), nat.ptr(_i32(widths, device)), float(scale),
-        int(split_tokens), int(units), nat.ptr(workspace),
-        0 if workspace is None else workspace.numel(), nat.ptr(out))
+        int(waves), nat.ptr(workspace), workspace.numel(), nat.ptr(out))
     nat.check(code, "paged attention")
     return out
 

@@ -79,6 +79,5 @@ def paged_attention(queries, rows, positions, widths, *, scale, _table=None):
                                   q_pos=torch.tensor([list(p) for p in positions], dtype=torch.int32,
                                                      device=device),
                                   widths=torch.tensor(list(widths), dtype=torch.int32,
-                                                      device=device),
-                                  lengths_host=lengths)
+                                                      device=device))
         return out.to(dtype)

@@ -70,20 +70,22 @@ def test_invalid_layouts_are_rejected(kw):
 
 def test_workspace_size():
     lib = nat.load()
-    # 100 partitions x 8 KV heads x 4 rows x (128 floats + 2 floats)
+    # 2 slots per wave x 100 waves x 4 rows x (128 + 2) floats
     need = lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 100)
-    assert need >= 100 * 8 * 4 * (128 + 2) * 4
+    assert need >= 2 * 100 * 4 * (128 + 2) * 4
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 0) < 0     # no waves
+    assert lib.pkv_attention_workspace_bytes(_layout(), 30, 1, 10) < 0    # not GQA groups
 
 
 def _attention(lib, layout, **kw):
     args = dict(stream=None, pool=FAKE, num_pages=10, q=FAKE, batch=2, heads=32, nq=1, table=FAKE,
-                max_pages=4, lens=FAKE, q_pos=None, widths=None, scale=0.1, split=0, units=2,
+                max_pages=4, lens=FAKE, q_pos=None, widths=None, scale=0.1, waves=3,
                 ws=None, ws_bytes=0, out=FAKE)
     args.update(kw)
     return lib.pkv_paged_attention(args["stream"], layout, args["pool"], args["num_pages"],
                                    args["q"], args["batch"], args["heads"], args["nq"],
                                    args["table"], args["max_pages"], args["lens"], args["q_pos"],
-                                   args["widths"], args["scale"], args["split"], args["units"],
+                                   args["widths"], args["scale"], args["waves"],
                                    args["ws"], args["ws_bytes"], args["out"])
 
 
@@ -91,10 +93,10 @@ def _attention(lib, layout, **kw):
     (dict(heads=30), nat.PKV_UNSUPPORTED),                      # not a GQA multiple of HK=8
     (dict(nq=9), nat.PKV_UNSUPPORTED),                          # 9 x 4 = 36 rows > 32
     (dict(pool=None), nat.PKV_INVALID_ARGUMENT),
-    (dict(split=24), nat.PKV_INVALID_ARGUMENT),                 # not a page multiple
-    (dict(split=16 * 65), nat.PKV_INVALID_ARGUMENT),            # more than 64 pages
-    (dict(units=1), nat.PKV_INVALID_ARGUMENT),                  # fewer units than sequences
-    (dict(units=3), nat.PKV_OUT_OF_MEMORY),                     # split-K needs a workspace
+    (dict(num_pages=0), nat.PKV_INVALID_ARGUMENT),
+    (dict(waves=3), nat.PKV_OUT_OF_MEMORY),                     # the merge needs a workspace
+    (dict(waves=3, ws=FAKE, ws_bytes=64), nat.PKV_OUT_OF_MEMORY),
+    (dict(waves=1 << 25, ws=FAKE, ws_bytes=1 << 40), nat.PKV_INVALID_ARGUMENT),
     (dict(scale=float("inf")), nat.PKV_INVALID_ARGUMENT),
     (dict(batch=-1), nat.PKV_INVALID_ARGUMENT),
     (dict(batch=0), nat.PKV_OK),

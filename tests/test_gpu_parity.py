@@ -157,18 +157,25 @@ def test_copy_pages_duplicates_page_bytes():
 
 
 ATTN_CASES = {
-    # name: (workload overrides, dtype, chunk, split_tokens)
+    # name: (workload overrides, dtype, chunk, waves); waves 0 = the device's
+    # resident capacity, small counts split most (sequence, KV head) pairs
+    # into pieces merged in-kernel, 1 runs everything through one wave
     "c1_bf16": (dict(name="c1"), "bfloat16", 64, 0),
-    "c1_bf16_split": (dict(name="c1"), "bfloat16", 128, 64),
+    "c1_bf16_waves5": (dict(name="c1"), "bfloat16", 128, 5),
     "c2_small": (dict(name="c2", batch=4, length_range=(1, 900)), "bfloat16", 100, 0),
-    "c2_small_split": (dict(name="c2", batch=5, length_range=(17, 700)), "bfloat16", 50, 128),
-    "c2_g32_f16": (dict(name="c2", batch=3, length_range=(100, 400), group_size=32), "float16", 64, 64),
-    "c3_small": (dict(name="c3", batch=2, lengths=(1500, 2048)), "bfloat16", 512, 512),
+    "c2_small_waves13": (dict(name="c2", batch=5, length_range=(17, 700)), "bfloat16", 50, 13),
+    "c2_g32_f16": (dict(name="c2", batch=3, length_range=(100, 400), group_size=32), "float16",
+                   64, 3),
+    "c2_one_wave_long": (dict(name="c2", batch=2, lengths=(2100, 1500)), "bfloat16", 256, 1),
+    "c3_small": (dict(name="c3", batch=2, lengths=(1500, 2048)), "bfloat16", 512, 0),
+    "c3_partitions512": (dict(name="c3", batch=2, lengths=(2048, 2048)), "bfloat16", 512, 32),
+    "c3_one_wave_long": (dict(name="c3", batch=1, lengths=(4100,)), "bfloat16", 512, 1),
     "c4_small": (dict(name="c4", batch=4, length_range=(300, 700)), "bfloat16", 128, 0),
-    "c4_split": (dict(name="c4", batch=3, length_range=(260, 520)), "bfloat16", 64, 64),
+    "c4_waves9": (dict(name="c4", batch=3, length_range=(260, 520)), "bfloat16", 64, 9),
     "d37_int8": (dict(name="c2", batch=3, length_range=(20, 200), head_dim=37, group_size=32),
-                 "bfloat16", 40, 32),
-    "f16_pages": (dict(name="c1", bits=16), "float16", 64, 32),
+                 "bfloat16", 40, 2),
+    "f16_pages": (dict(name="c1", bits=16), "float16", 64, 1),
+    "more_waves_than_tiles": (dict(name="c2", batch=2, lengths=(40, 3)), "bfloat16", 16, 10000),
 }
 
 
@@ -176,7 +183,7 @@ ATTN_CASES = {
 def test_attention_matches_oracle(case):
     from pkv import ops, workloads
 
-    overrides, dtype, chunk, split = ATTN_CASES[case]
+    overrides, dtype, chunk, waves = ATTN_CASES[case]
     overrides = dict(overrides)
     w = workloads.get(overrides.pop("name"), **overrides)
     inst = workloads.generate(w)
@@ -191,7 +198,7 @@ def test_attention_matches_oracle(case):
     scale = scale_of(w.head_dim)
     q = to_torch(inst.queries, fmt.dtype)
     out = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale,
-                              q_pos=torch.from_numpy(positions).cuda(), split_tokens=split)
+                              q_pos=torch.from_numpy(positions).cuda(), waves=waves)
     torch.cuda.synchronize()
     want = oracle_attention(fmt, inst, positions, widths, scale)
     assert_attention_close(out.float().cpu().numpy(), want)
@@ -209,7 +216,7 @@ def test_attention_padded_query_rows_are_zero():
     scale = scale_of(w.head_dim)
     out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
                               scale=scale, q_pos=torch.from_numpy(positions).cuda(),
-                              widths=torch.from_numpy(widths).cuda(), split_tokens=64)
+                              widths=torch.from_numpy(widths).cuda(), waves=11)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     want = oracle_attention(fmt, inst, positions, widths, scale)

@@ -145,12 +145,13 @@ def test_workloads_are_seeded_and_follow_configs():
     assert c4.positions.shape == (16, 5)
 
 
-def test_partition_planner():
-    split, units = ops.plan_partitions([100, 5000, 0], 16, 8)
-    assert split % 16 == 0 and 128 <= split <= 1024
-    assert units == sum(max(1, math.ceil(x / split)) for x in [100, 5000, 0])
-    split, units = ops.plan_partitions([32768] * 8, 32, 4, split_tokens=512)
-    assert (split, units) == (512, 8 * 64)
+def test_workload_waves():
+    """C3's 512-token partitions as waves: one per partition of every (sequence, KV head)."""
+    import bench
+
+    c3 = workloads.get("c3")
+    assert bench.workload_waves(c3, [32768] * 8) == 8 * 64 * 4
+    assert bench.workload_waves(workloads.get("c2"), [5000] * 32) == 0   # device capacity
 
 
 def test_bench_bytes_match_the_configs():
