@@ -31,6 +31,19 @@ for _p in (ROOT / "mlx-one_amd", ROOT):
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 
 
+def measured_traffic(workload):
+    """HBM bytes per attention launch measured with rocprofv3 PMC counters
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), as recorded in
+    profiles/pkv_attention_<workload>_traffic.md; None when not profiled."""
+    path = ROOT / "profiles" / f"pkv_attention_{workload}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def kv_bytes_per_token(w):
     """K+V bytes of one cached token: 2*HK*(D*bits/8 + (D/G)*4), or 2*HK*D*2 for bf16."""
     if w.bits == 16:
@@ -314,8 +327,9 @@ def main(argv=None):
     if attn_ms:
         achieved = attn_bytes / (attn_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "pkv_paged_attention (attn_kernel, merge fused)",
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic(w.name),
+                    "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     result = {
         "metric": "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)",

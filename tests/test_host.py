@@ -169,3 +169,16 @@ def test_bench_bytes_match_the_configs():
     assert bench.kv_bytes_per_token(w3) == 576
     attn3, _ = bench.algorithmic_bytes(w3, [32768] * 8)
     assert attn3 - 4 * 8 * 1024 == 150_994_944 + 131_072
+
+
+def test_profiled_traffic_matches_algorithmic_bytes():
+    """The committed PMC profile of the C2 attention launch: HBM traffic within
+    5% of the algorithmic bytes (no re-reads), as bench.py reports it."""
+    import bench
+
+    traffic = bench.measured_traffic("c2")
+    assert traffic is not None
+    w = workloads.get("c2")
+    inst = workloads.generate(w, kv=False)
+    attn, _ = bench.algorithmic_bytes(w, inst.context + w.append_tokens)
+    assert 1.0 <= traffic / attn < 1.05
