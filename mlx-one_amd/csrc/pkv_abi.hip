@@ -45,6 +45,9 @@ int geometry(const pkv_layout *layout, pkv_geometry *g) {
   return PKV_OK;
 }
 
+// Query rows per KV head (queries x heads per KV head) one call may carry.
+constexpr int64_t kMaxRows = 1 << 24;
+
 // Attention workspace: [ml: S*rows*2 f32][acc: S*rows*DP f32] with
 // S = kSlotsPerWave * waves partial slots, each part 256-byte aligned.
 struct WorkspaceParts {
@@ -131,9 +134,10 @@ int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t
   pkv_geometry g;
   if (geometry(layout, &g) != PKV_OK) return -1;
   if (num_heads < 1 || num_queries < 1 || num_heads % g.hk) return -1;
-  const int rows = num_queries * (num_heads / g.hk);
-  if (rows > 32) return -1;
-  const int w = cached_waves(g, rows);
+  const int64_t rows = (int64_t)num_queries * (num_heads / g.hk);
+  if (rows > kMaxRows) return -1;
+  if (!pkv::decode_serves(pkv::to_geo(g), (int)rows)) return 1;  // prefill kernel: no split
+  const int w = cached_waves(g, (int)rows);
   if (w <= 0) {
     fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
     return -1;
@@ -148,6 +152,8 @@ int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_head
       waves < 1)
     return -1;
   const int64_t rows = (int64_t)num_queries * (num_heads / g.hk);
+  if (rows > kMaxRows) return -1;
+  if (!pkv::decode_serves(pkv::to_geo(g), (int)rows)) return 0;  // prefill kernel: no partials
   return workspace_parts(g, rows, waves).total;
 }
 
@@ -163,23 +169,50 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   if (num_heads < 1 || num_queries < 1 || num_heads % geo.hk)
     return fail(PKV_UNSUPPORTED, "paged attention requires query heads to form valid GQA groups");
   const int gqa = num_heads / geo.hk;
-  const int rows = num_queries * gqa;
-  if (rows > 32)
-    return fail(PKV_UNSUPPORTED, "paged attention supports at most 32 query rows per KV head "
+  if ((int64_t)num_queries * gqa > kMaxRows)
+    return fail(PKV_UNSUPPORTED, "paged attention supports at most 2^24 query rows per KV head "
                                  "(queries x heads per KV head)");
+  const int rows = num_queries * gqa;
   if (!pool || !queries || !block_table || !seq_lens || !out)
     return fail(PKV_INVALID_ARGUMENT, "paged attention requires pool, queries, block table, lengths, out");
   if (num_pages < 1 || max_pages < 1) return fail(PKV_INVALID_ARGUMENT, "empty page pool or block table");
   if (!std::isfinite(scale)) return fail(PKV_INVALID_ARGUMENT, "softmax scale must be finite");
+  // the kernels number 16-token tiles in int32: bound them by the block table
+  const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16);
+  if ((int64_t)batch * tiles_per_seq * geo.hk > INT32_MAX / 2)
+    return fail(PKV_UNSUPPORTED, "paged attention batch too large (more than 2^30 tiles)");
+  if (!pkv::decode_serves(pkv::to_geo(geo), rows)) {
+    // wide query blocks (chunked prefill): one pass per (sequence, KV head,
+    // 128-row block), no partials; waves and the workspace are not used
+    if ((int64_t)batch * geo.hk * ((rows + 127) / 128) > INT32_MAX)
+      return fail(PKV_UNSUPPORTED, "paged attention grid too large");
+    pkv::AttnArgs a;
+    a.g = pkv::to_geo(geo);
+    a.pool = (const uint8_t *)pool;
+    a.num_pages = num_pages;
+    a.q = (const uint16_t *)queries;
+    a.batch = batch;
+    a.heads = num_heads;
+    a.nq = num_queries;
+    a.gqa = gqa;
+    a.rows = rows;
+    a.table = block_table;
+    a.max_pages = max_pages;
+    a.seq_lens = seq_lens;
+    a.q_pos = q_pos;
+    a.widths = widths;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.waves = 0;
+    a.part_ml = nullptr;
+    a.part_acc = nullptr;
+    a.out = (uint16_t *)out;
+    return check_launch(pkv::launch_prefill((hipStream_t)stream, a), "prefill launch");
+  }
   if (waves <= 0) {
     waves = cached_waves(geo, rows);
     if (waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
   }
   if (waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
-  // the kernel numbers 16-token tiles in int32: bound them by the block table
-  const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16);
-  if ((int64_t)batch * tiles_per_seq * geo.hk > INT32_MAX / 2)
-    return fail(PKV_UNSUPPORTED, "paged attention batch too large (more than 2^30 tiles)");
   const WorkspaceParts parts = workspace_parts(geo, rows, waves);
   if (!workspace || workspace_bytes < parts.total)
     return fail(PKV_OUT_OF_MEMORY,

@@ -78,8 +78,13 @@ hipError_t launch_copy(hipStream_t stream, uint8_t *pool, int64_t num_pages, int
                        const int32_t *src, const int32_t *dst, int count);
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a);
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a);
+// Query blocks wider than the decode kernel serves (chunked prefill).
+hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a);
 // Resident waves of the attention kernel for this layout and row count on the
 // current device (CUs x workgroups per CU); <0 on error.
 int attention_waves(const Geo &g, int rows);
+// Whether the split-K decode kernel serves this many rows per KV head (else
+// launch_prefill does, with no workspace and no merge).
+bool decode_serves(const Geo &g, int rows);
 
 }  // namespace pkv

@@ -1,0 +1,143 @@
+// pkv_mfma.h -- MFMA operand plumbing shared by the paged attention kernels
+// (gfx950): tile geometry, lane payload/metadata loads, code->f16 operand
+// conversion and the f16/bf16 MFMA wrappers.
+//
+// A 16-token tile of K (or V) stores lane l's MFMA operand bytes at
+// tile + c*1024 + l*16 (16-byte chunks).  Codes become f16 operands as
+// 1024 + c: two u8 codes per v_perm against the 0x64 exponent byte, two 4-bit
+// codes per mask-and-or.  The K scale and bias are applied to the score tile
+// after the MFMA, the V scale is folded into the P operand.
+#pragma once
+#include "pkv_launch.h"
+
+namespace pkv {
+
+constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units)
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+// Two u8 codes -> f16 pair (1024 + c0, 1024 + c1): bytes 0,1 (sel_lo) or 2,3 (sel_hi).
+constexpr uint32_t kMagic = 0x64646464u;
+constexpr uint32_t kSelLo = 0x00050004u;
+constexpr uint32_t kSelHi = 0x00070006u;
+
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
+struct Cfg {
+  static constexpr bool QUANT = BITS != 16;
+  static constexpr int NG = QUANT ? DP / G : 1;
+  static constexpr int KB = DP / 32;
+  static constexpr int NB = DP / 16;
+  static constexpr int RPS = 16 / SLOTS;  // query rows (columns) per slot
+  static constexpr int LB = DP * BITS / 32;  // payload bytes per lane and side
+  static constexpr int LW = LB / 4;
+  static constexpr int CS = LB < 16 ? LB : 16;
+  static constexpr int NCH = LB / CS;
+  static constexpr int MW = QUANT ? 4 * NG : 4;  // meta dwords per lane (4 tokens x NG)
+  static_assert(SLOTS == 1 || RB == 1, "column slots need a single row block");
+  static_assert(CS == 16 || (CS == 8 && NCH == 1), "payload chunk");
+};
+
+// A lane's K or V payload of one tile, straight from HBM.
+template <typename C>
+__device__ __forceinline__ void load_payload(uint32_t (&w)[C::LW], const uint8_t *tile, int lane) {
+  if constexpr (C::CS == 16) {
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) {
+      const u4 x = *(const u4 *)(tile + c * 1024 + lane * 16);
+      w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
+    }
+  } else {
+    const u2 x = *(const u2 *)(tile + lane * 8);
+    w[0] = x.x; w[1] = x.y;
+  }
+}
+
+// The metadata words (all groups) of a lane's four tokens: 4*NG contiguous dwords.
+template <typename C>
+__device__ __forceinline__ void load_meta(uint32_t (&mw)[C::MW], const uint8_t *p) {
+#pragma unroll
+  for (int i = 0; i < C::MW; i += 4) {
+    const u4 x = *(const u4 *)(p + i * 4);
+    mw[i] = x.x; mw[i + 1] = x.y; mw[i + 2] = x.z; mw[i + 3] = x.w;
+  }
+}
+
+template <int BITS>
+struct Conv;
+
+template <>
+struct Conv<8> {
+  template <int LW>
+  static __device__ __forceinline__ h8 kop(const uint32_t (&w)[LW], int kb) {
+    const uint32_t w0 = w[2 * kb], w1 = w[2 * kb + 1];
+    u4 r = {perm(w0, kMagic, kSelLo), perm(w0, kMagic, kSelHi), perm(w1, kMagic, kSelLo),
+            perm(w1, kMagic, kSelHi)};
+    return __builtin_bit_cast(h8, r);
+  }
+  template <int LW>
+  static __device__ __forceinline__ h4 vop(const uint32_t (&w)[LW], int n) {
+    const uint32_t w0 = w[n];
+    u2 r = {perm(w0, kMagic, kSelLo), perm(w0, kMagic, kSelHi)};
+    return __builtin_bit_cast(h4, r);
+  }
+};
+
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int s) {
+  return ((w >> (4 * s)) & 0x000F000Fu) | 0x64006400u;
+}
+
+template <>
+struct Conv<4> {
+  template <int LW>
+  static __device__ __forceinline__ h8 kop(const uint32_t (&w)[LW], int kb) {
+    const uint32_t x = w[kb];
+    u4 r = {nib_pair(x, 0), nib_pair(x, 1), nib_pair(x, 2), nib_pair(x, 3)};
+    return __builtin_bit_cast(h8, r);
+  }
+  template <int LW>
+  static __device__ __forceinline__ h4 vop(const uint32_t (&w)[LW], int n) {
+    const uint32_t x = w[n >> 1];
+    const int o = n & 1;
+    u2 r = {nib_pair(x, o), nib_pair(x, 2 + o)};
+    return __builtin_bit_cast(h4, r);
+  }
+};
+
+template <int FK>
+struct FloatOps;
+
+template <>
+struct FloatOps<1> {  // f16 operands (f16 pages, and codes of quantized pages)
+  typedef h8 KT;
+  typedef h4 VT;
+  static __device__ __forceinline__ f4 qk(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f4 pv(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ h4 pack_p(float p0, float p1, float p2, float p3) {
+    return h4{(_Float16)p0, (_Float16)p1, (_Float16)p2, (_Float16)p3};
+  }
+};
+
+template <>
+struct FloatOps<0> {  // bf16 pages
+  typedef b8 KT;
+  typedef s4 VT;
+  static __device__ __forceinline__ f4 qk(b8 a, b8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f4 pv(s4 a, s4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ s4 pack_p(float p0, float p1, float p2, float p3) {
+    return s4{(short)f32_to_bf16_bits(p0), (short)f32_to_bf16_bits(p1),
+              (short)f32_to_bf16_bits(p2), (short)f32_to_bf16_bits(p3)};
+  }
+};
+
+
+}  // namespace pkv

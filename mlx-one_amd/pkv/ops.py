@@ -17,7 +17,6 @@ from pkv import _native as nat
 
 FLOAT_KINDS = {torch.bfloat16: 0, torch.float16: 1}
 DTYPES = {0: torch.bfloat16, 1: torch.float16}
-MAX_ROWS = 32          # query rows (queries x heads per KV head) per attention launch
 
 
 @dataclass(frozen=True)
@@ -154,27 +153,6 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     if queries.dim() != 4:
         raise ValueError("queries must be [B, H, Q, D]")
     batch, heads, nq, dim = queries.shape
-    group = heads // max(fmt.num_kv_heads, 1)
-    per_launch = max(1, MAX_ROWS // max(group, 1))
-    if heads % fmt.num_kv_heads == 0 and nq > per_launch:
-        # wide query blocks (prefill) run as launches of <= MAX_ROWS rows per KV head
-        device = queries.device
-        lens = _i32(seq_lens, device)
-        pos = _i32(q_pos, device) if q_pos is not None else (
-            lens[:, None] - (_i32(widths, device)[:, None] if widths is not None else nq)
-            + torch.arange(nq, device=device, dtype=torch.int32)[None])
-        wid = _i32(widths, device) if widths is not None else torch.full(
-            (batch,), nq, dtype=torch.int32, device=device)
-        if out is None:
-            out = torch.empty_like(queries)
-        for s in range(0, nq, per_launch):
-            e = min(nq, s + per_launch)
-            part = paged_attention(fmt, pool, queries[:, :, s:e].contiguous(), block_table, lens,
-                                   scale=scale, q_pos=pos[:, s:e].contiguous(),
-                                   widths=(wid - s).clamp(0, e - s), waves=waves,
-                                   workspace=workspace)
-            out[:, :, s:e] = part
-        return out
     if dim != fmt.head_dim:
         raise ValueError("query head dimension differs from the page layout")
     _check_float(queries, fmt, "queries")

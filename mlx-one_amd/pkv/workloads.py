@@ -55,6 +55,12 @@ CONFIGS = {
                    shared_prefix_pages=16, seed=3,
                    description="int8 speculative verify, B16 Q5 causal drafts, 256-token "
                                "shared prefix"),
+    "c5": Workload("c5", batch=4, heads=32, kv_heads=8, head_dim=128, page_tokens=16, bits=8,
+                   group_size=64, num_queries=512, append_tokens=512, lengths=(4096,) * 4,
+                   seed=4,
+                   description="int8 G64 chunked prefill: 512-token causal query chunk per "
+                               "sequence over a 4096-token paged prefix plus the chunk, B4 "
+                               "H32/HK8 D128 P16"),
 }
 
 

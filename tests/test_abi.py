@@ -75,6 +75,12 @@ def test_workspace_size():
     assert need >= 2 * 100 * 4 * (128 + 2) * 4
     assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 0) < 0     # no waves
     assert lib.pkv_attention_workspace_bytes(_layout(), 30, 1, 10) < 0    # not GQA groups
+    # query blocks past the decode kernel's 32 rows per KV head run on the
+    # prefill kernel: no split, no partials
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 9, 10) == 0
+    assert lib.pkv_attention_waves(_layout(), 32, 512) == 1
+    assert lib.pkv_attention_waves(_layout(head_dim=256), 32, 5) == 1     # 20 rows at D=256
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1 << 23, 10) < 0
 
 
 def _attention(lib, layout, **kw):
@@ -91,7 +97,8 @@ def _attention(lib, layout, **kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(heads=30), nat.PKV_UNSUPPORTED),                      # not a GQA multiple of HK=8
-    (dict(nq=9), nat.PKV_UNSUPPORTED),                          # 9 x 4 = 36 rows > 32
+    (dict(nq=1 << 23), nat.PKV_UNSUPPORTED),                    # 2^25 rows per KV head
+    (dict(nq=9, pool=None), nat.PKV_INVALID_ARGUMENT),          # prefill route validates too
     (dict(pool=None), nat.PKV_INVALID_ARGUMENT),
     (dict(num_pages=0), nat.PKV_INVALID_ARGUMENT),
     (dict(waves=3), nat.PKV_OUT_OF_MEMORY),                     # the merge needs a workspace

@@ -176,6 +176,36 @@ ATTN_CASES = {
                  "bfloat16", 40, 2),
     "f16_pages": (dict(name="c1", bits=16), "float16", 64, 1),
     "more_waves_than_tiles": (dict(name="c2", batch=2, lengths=(40, 3)), "bfloat16", 16, 10000),
+    # wide query blocks (> 32 rows per KV head, or > 16 at head_dim 256) run
+    # on the chunked-prefill kernel: 128-row blocks, causal over the chunk
+    "prefill_c5_small": (dict(name="c5", batch=2, lengths=(300, 170), num_queries=128,
+                              append_tokens=128), "bfloat16", 64, 0),
+    "prefill_partial_block": (dict(name="c5", batch=2, lengths=(33, 0), num_queries=37,
+                                   append_tokens=37), "bfloat16", 16, 0),
+    "prefill_g32_f16": (dict(name="c5", batch=2, lengths=(90, 260), num_queries=64,
+                             append_tokens=64, group_size=32), "float16", 100, 0),
+    "prefill_g128": (dict(name="c5", batch=1, lengths=(200,), num_queries=40, append_tokens=40,
+                          group_size=128), "bfloat16", 80, 0),
+    "prefill_4bit_p32": (dict(name="c5", batch=2, lengths=(500, 77), num_queries=96,
+                              append_tokens=96, bits=4, page_tokens=32), "bfloat16", 128, 0),
+    "prefill_4bit_d64_p64": (dict(name="c5", batch=2, lengths=(129, 64), num_queries=48,
+                                  append_tokens=48, bits=4, head_dim=64, group_size=32,
+                                  page_tokens=64), "bfloat16", 64, 0),
+    "prefill_d37": (dict(name="c5", batch=2, lengths=(60, 150), num_queries=33, append_tokens=33,
+                         head_dim=37, group_size=32), "bfloat16", 40, 0),
+    "prefill_d256_rows20": (dict(name="c5", batch=3, lengths=(100, 260, 31), num_queries=5,
+                                 append_tokens=5, head_dim=256, group_size=128), "bfloat16",
+                            64, 0),
+    "prefill_d256_4bit": (dict(name="c5", batch=2, lengths=(140, 50), num_queries=20,
+                               append_tokens=20, head_dim=256, bits=4, group_size=32),
+                          "bfloat16", 64, 0),
+    "prefill_bf16_pages": (dict(name="c5", batch=2, lengths=(180, 20), num_queries=64,
+                                append_tokens=64, bits=16), "bfloat16", 64, 0),
+    "prefill_f16_pages_d64": (dict(name="c5", batch=2, lengths=(70, 130), num_queries=40,
+                                   append_tokens=40, bits=16, head_dim=64), "float16", 32, 0),
+    "prefill_bf16_pages_d100": (dict(name="c5", batch=1, lengths=(150,), num_queries=36,
+                                     append_tokens=36, bits=16, head_dim=100), "bfloat16",
+                                50, 0),
 }
 
 
@@ -222,3 +252,30 @@ def test_attention_padded_query_rows_are_zero():
     want = oracle_attention(fmt, inst, positions, widths, scale)
     assert_attention_close(got, want)
     assert np.all(got[1, :, 2:] == 0) and np.all(got[2, :, 1:] == 0)
+
+
+@pytest.mark.parametrize("positions_given", [True, False])
+def test_prefill_ragged_widths(positions_given):
+    """Chunks of different widths in one call: rows past a sequence's width are 0.
+
+    Without ``q_pos`` query q of a width-w chunk sits at position L - w + q.
+    """
+    from pkv import ops, workloads
+
+    w = workloads.get("c5", batch=3, lengths=(120, 40, 300), num_queries=48, append_tokens=48)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    widths = np.array([48, 17, 1], np.int32)
+    total = inst.total_lengths
+    positions = np.stack([total[b] - widths[b] + np.arange(w.num_queries) for b in range(w.batch)])
+    positions = positions.astype(np.int32)
+    scale = scale_of(w.head_dim)
+    q_pos = torch.from_numpy(positions).cuda() if positions_given else None
+    out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
+                              scale=scale, q_pos=q_pos, widths=torch.from_numpy(widths).cuda())
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = oracle_attention(fmt, inst, positions, widths, scale)
+    assert_attention_close(got, want)
+    assert np.all(got[1, :, 17:] == 0) and np.all(got[2, :, 1:] == 0)

@@ -143,6 +143,9 @@ def test_workloads_are_seeded_and_follow_configs():
     c4 = workloads.generate(workloads.get("c4"), kv=False)
     assert np.all(c4.table[:, :16] == c4.table[0, :16])       # 256-token shared prefix
     assert c4.positions.shape == (16, 5)
+    c5 = workloads.generate(workloads.get("c5"), kv=False)
+    assert c5.positions.shape == (4, 512)
+    assert np.all(c5.positions[:, 0] == 4096) and np.all(c5.positions[:, -1] == 4607)
 
 
 def test_workload_waves():
