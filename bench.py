@@ -29,6 +29,7 @@ for _p in (ROOT / "mlx-one_amd", ROOT):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA (no sparsity)
 
 
 def measured_traffic(workload):
@@ -66,6 +67,20 @@ def algorithmic_bytes(w, lengths):
     attention = kv + qo + table
     new_rows = w.batch * w.append_tokens * 2 * w.kv_heads * w.head_dim * 2
     return attention, attention + new_rows
+
+
+def is_prefill(w):
+    """Query blocks past 32 rows per KV head run on the MFMA prefill kernel."""
+    return w.num_queries * (w.heads // w.kv_heads) > 32
+
+
+def attention_flops(w, lengths):
+    """Causal-exact flops of one attention launch: 4*D per (query row, visible
+    token) for QK^T and PV.  Query q of a chunk of Q sits at L - Q + q and sees
+    L - Q + q + 1 tokens, so a sequence costs 4*D*H*(Q*(L - Q) + Q*(Q + 1)/2)."""
+    q = w.num_queries
+    pairs = sum(q * (int(x) - q) + q * (q + 1) // 2 for x in lengths)
+    return 4.0 * w.head_dim * w.heads * pairs
 
 
 class Layer:
@@ -140,8 +155,8 @@ def cpu_baseline(w, inst, layer, device, budget_s):
         full[used] = a
         host.append(full)
     lengths = inst.context + w.append_tokens
-    positions = (lengths - 1).reshape(-1, 1).astype(np.int32)
-    widths = np.ones(w.batch, np.int32)
+    positions = (lengths[:, None] - w.num_queries + np.arange(w.num_queries)[None]).astype(np.int32)
+    widths = np.full(w.batch, w.num_queries, np.int32)
     q = layer.queries.float().cpu().numpy()
     scale = 1.0 / math.sqrt(w.head_dim)
 
@@ -157,10 +172,17 @@ def cpu_baseline(w, inst, layer, device, budget_s):
                                      bits=w.bits, group_size=w.group_size, pages=host,
                                      scale=scale, threads=cores)
 
-    started = time.perf_counter()
-    want = run(w.batch)                       # warm-up and a full-step reference
-    first = time.perf_counter() - started
-    rows = w.batch
+    if is_prefill(w):
+        # a bounded sample: the first sequence's whole chunk
+        rows = 1
+        started = time.perf_counter()
+        want = run(rows)
+        first = time.perf_counter() - started
+    else:
+        started = time.perf_counter()
+        want = run(w.batch)                   # warm-up and a full-step reference
+        first = time.perf_counter() - started
+        rows = w.batch
     reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
     times = []
     for _ in range(reps):
@@ -168,6 +190,15 @@ def cpu_baseline(w, inst, layer, device, budget_s):
         run(rows)
         times.append(time.perf_counter() - t0)
     step_s = float(np.median(times))
+    if is_prefill(w):
+        return {"value": rows * w.num_queries / step_s, "unit": "tok/s", "cores": cores,
+                "kind": "port",
+                "sample": f"{w.name} step of {rows} of {w.batch} sequences (quantize its "
+                          f"{w.append_tokens} new K/V rows + causal attention of its "
+                          f"{w.num_queries}-token chunk over {int(lengths[0])} tokens), median "
+                          f"of {reps}, OpenMP C restatement (oracle/pkv_oracle.c) on "
+                          f"reference-format pages",
+                "ms_per_step": step_s * 1e3}, want
     return {"value": rows / step_s, "unit": "seqs*tok/s", "cores": cores, "kind": "port",
             "sample": f"full {w.name} step ({rows} sequences, 1 layer: quantize the new K/V "
                       f"rows + attention over {int(lengths.sum())} cached tokens), median of "
@@ -235,7 +266,7 @@ def main(argv=None):
     torch.cuda.set_device(device)
     w = workloads.get(args.workload)
     total_steps = args.warmup + args.steps
-    growth = math.ceil(total_steps / args.layers) * w.append_tokens
+    growth = 0 if w.fixed_chunk else math.ceil(total_steps / args.layers) * w.append_tokens
     inst = workloads.generate(w, extra_tokens=growth, kv=False)
     fmt = ops.PageFormat(w.kv_heads, w.head_dim, w.page_tokens, w.bits, w.group_size,
                          torch.bfloat16)
@@ -250,7 +281,7 @@ def main(argv=None):
     plans = []
     for s in range(total_steps):
         li = s % args.layers
-        start = context + (s // args.layers) * w.append_tokens
+        start = context + (0 if w.fixed_chunk else (s // args.layers) * w.append_tokens)
         lens = start + w.append_tokens
         plans.append((li, torch.from_numpy(start.astype(np.int32)).to(device),
                       torch.from_numpy(lens.astype(np.int32)).to(device),
@@ -322,33 +353,52 @@ def main(argv=None):
     timed = plans[args.warmup:]
     mean_lens = np.mean([p[3] for p in timed], axis=0)
     attn_bytes, step_bytes = algorithmic_bytes(w, mean_lens)
-    value = w.batch / (ms_per_step / 1e3)
+    prefill = is_prefill(w)
+    value = w.batch * (w.num_queries if prefill else 1) / (ms_per_step / 1e3)
     roofline = None
-    if attn_ms:
+    if attn_ms and prefill:
+        flops = attention_flops(w, mean_lens)
+        achieved = flops / (attn_ms / 1e3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
+                    "traffic": measured_traffic(w.name),
+                    "kernel": "pkv_paged_attention (prefill_kernel)",
+                    "kernel_ms": round(attn_ms, 5), "flops_per_launch": int(flops),
+                    "bytes_per_launch": int(attn_bytes),
+                    "hbm_gbs": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1)}
+    elif attn_ms:
         achieved = attn_bytes / (attn_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(w.name),
                     "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
+    if prefill:
+        metric = "chunked-prefill attention query tok/s (int8 paged KV, 1 layer)"
+        unit = "tok/s"
+    else:
+        metric = "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)"
+        unit = "seqs*tok/s"
     result = {
-        "metric": "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)",
-        "value": round(value, 1), "unit": "seqs*tok/s", "n_gpus": 1, "steps": args.steps,
+        "metric": metric,
+        "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if w.bits == 8 else f"u{w.bits}",
         "data": "synthetic",
         "config": {"workload": w.name, "batch": w.batch, "heads": w.heads,
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
-                   "bits": w.bits, "group_size": w.group_size, "mean_context": float(mean_lens.mean()),
+                   "bits": w.bits, "group_size": w.group_size, "num_queries": w.num_queries,
+                   "mean_context": float(mean_lens.mean()),
                    "waves": waves, "layers_rotated": args.layers, "graph": args.graph},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
     }
     if args.cpu_budget > 0:
         base, want = cpu_baseline(w, inst, layers[0], device, args.cpu_budget)
-        got = check_step
+        got = check_step[:want.shape[0]]
         # The oracle reads the pool after all steps; later steps only wrote
-        # positions past step 0's lengths, which the oracle does not read.
+        # positions past step 0's lengths (or, for a fixed chunk, the same
+        # chunk again), which leaves what the oracle reads unchanged.
         err = np.abs(got - workloads.bf16_round(want.reshape(got.shape)))
         base["check_vs_gpu"] = {"max_abs": float(err.max()), "mean_abs": float(err.mean())}
         result["cpu_baseline"] = base

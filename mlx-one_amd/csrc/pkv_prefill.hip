@@ -8,103 +8,107 @@
 // 512 queries x 4 heads = 2048 rows per KV head), where the contraction is
 // dense and MFMA-bound.
 //
-// Work unit = one workgroup of 4 waves = (sequence, KV head, block of 128
-// query rows); wave w owns rows 32w..32w+31 of the block as two 16-column
-// MFMA row tiles.  K/V tiles of 16 tokens are staged once per workgroup in LDS
-// (global_load_lds_dwordx4, 4 tiles per stage, double-buffered: each wave
-// DMAs one tile of the next stage while all four compute the current one) and
-// read by all four waves: every byte of KV is fetched from HBM once per 128
-// query rows.  Per tile and wave: S^T = K.Q^T (v_mfma_f32_16x16x32_f16 over the
-// codes as f16, per-group scale/bias applied to the score tile), online
-// softmax per column (exp2, lazy rescale), O^T += V^T.P' (v_mfma_f32_16x16x16).
-// Causal: stages past the block's last visible token are not loaded; tiles
-// every live row sees entirely skip the per-token mask.
+// Work unit = one workgroup of 4 waves = (sequence, KV head, block of 4*16*RB
+// query rows); wave w owns 16*RB rows as RB 16-column MFMA row tiles.  The
+// span is streamed in stages of 4 tiles (64 tokens).  Per stage each wave
+// loads ONE tile of quantized K/V (plus its scale/bias words) from HBM into
+// registers a stage ahead, dequantizes it once (packed f16: (1024+c) - 1024,
+// then c*scale + bias) and writes the f16 image into the LDS stage buffer
+// that all four waves read: K as [tile][token][dim], V transposed as
+// [dim][token slot].  Dequantization thus costs 1/4 tile per wave, and the
+// inner loop is a plain f16 flash-attention step:
+//   S^T = K.Q^T        v_mfma_f32_16x16x32_f16, two tiles per step
+//   online softmax     per column, exp2 domain, lazy rescale
+//   O^T += V^T.P^T     v_mfma_f32_16x16x32_f16 over the step's 32 tokens
+// The PV contraction pairs the two tiles' tokens: lane group jj holds tokens
+// 4jj..4jj+3 of each tile of its scores, and the V^T image stores those 8
+// tokens contiguously, so P needs no cross-lane movement.
+// Steps whose tiles every live row sees whole take a path without per-token
+// masks; tokens past the sequence or on unmapped pages are stored as zeros
+// and masked.
+#include <type_traits>
+
 #include "pkv_mfma.h"
 
 namespace pkv {
 
 constexpr int kPrefillWaves = 4;
-constexpr int kPrefillRows = kPrefillWaves * 32;  // query rows per workgroup
-constexpr int kStageTiles = kPrefillWaves;       // one tile DMA'd by each wave per stage
+constexpr int kStageTiles = kPrefillWaves;  // each wave converts one tile per stage
 
-typedef __attribute__((address_space(3))) void lds_void;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// Global -> LDS DMA of one 16- or 4-byte piece per lane: lane l's data lands
-// at dst + l*size (dst is wave-uniform).
-__device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void *src, uint8_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 4, 0, 0);
-}
+// Row blocks per wave: two 16-column blocks up to head_dim 128, one beyond
+// (register budget of the O accumulators).
+constexpr int prefill_rb(int dp) { return dp > 128 ? 1 : 2; }
+constexpr int prefill_rows(int dp) { return kPrefillWaves * 16 * prefill_rb(dp); }
 
-// Workgroup barrier once all but this wave's VM youngest vector-memory
-// operations (DMAs) have landed and its LDS operations have completed (s_waitcnt gfx9 encoding:
-// vmcnt VM, expcnt any, lgkmcnt 0).  No memory fence: __syncthreads() would
-// also drain the DMAs of the stage in flight.
-template <int VM>
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | ((VM >> 4) << 14));
+// LDS image of one stage (u16 elements).  Rows padded by 8 elements so that
+// the 16 lanes of a ds_read_b128 phase hit distinct banks.
+template <int DP>
+struct StageImage {
+  static constexpr int KROW = DP + 8;                // K row: one token
+  static constexpr int KTILE = 16 * KROW;
+  static constexpr int VROW = 16 * kStageTiles + 8;  // V^T row: one dim, 64 token slots
+  static constexpr int K_ELEMS = kStageTiles * KTILE;
+  static constexpr int ELEMS = K_ELEMS + DP * VROW;
+};
+
+// Workgroup barrier once this wave's LDS operations have completed.  No
+// memory fence: __syncthreads() would also wait for the next stage's HBM
+// loads still in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   asm volatile("s_barrier" ::: "memory");
 }
 
 // Page-table reads through the constant address space: uniform indices give
-// scalar loads, which do not count against vmcnt.
+// scalar loads.
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 
 template <int BITS, int DP, int G, int FK>
 __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
-  constexpr int RB = 2;
+  constexpr int RB = prefill_rb(DP);
+  constexpr int ROWS = prefill_rows(DP);
   using C = Cfg<BITS, DP, G, RB, FK, 1>;
   constexpr bool QUANT = C::QUANT;
-  constexpr int NG = C::NG, KB = C::KB, NB = C::NB;
-  using FO = FloatOps<QUANT ? 1 : FK>;
-  using KT = typename FO::KT;
-  using VT = typename FO::VT;
-  // LDS image of one tile: [K payload][V payload][K meta][V meta], the
-  // payload in the page's own lane order
-  constexpr int KP = C::LB * 64;
-  constexpr int META = QUANT ? 128 * NG : 0;
-  constexpr int SLOT = 2 * KP + META;
-  // LDS-DMA instructions per tile (each decrements vmcnt once)
-  constexpr int PAY = C::CS == 16 ? C::NCH : 2;
-  constexpr int METAI = QUANT ? (32 * NG + 63) / 64 : 0;
-  constexpr int LPT = 2 * PAY + METAI;
-  static_assert(LPT <= 63, "vmcnt range");
+  constexpr bool F16 = QUANT || FK == 1;  // f16 operands, else bf16
+  constexpr int NG = C::NG, KB = C::KB, NB = C::NB, LW = C::LW;
+  using I = StageImage<DP>;
+  typedef typename std::conditional<F16, h8, b8>::type OT;  // 8-element MFMA operand
+
   __shared__ int s_valid[2][kStageTiles];
   __shared__ int s_lim[2][kPrefillWaves];
-  // two stage buffers as distinct LDS objects: reads of one carry no
-  // dependence on DMAs in flight into the other
-  __shared__ __attribute__((aligned(16))) uint8_t stage0[kStageTiles][SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t stage1[kStageTiles][SLOT];
+  __shared__ __attribute__((aligned(16))) uint16_t stage[2][I::ELEMS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, jj = lane >> 4;
   const Geo &g = a.g;
-  const int nblk = (a.rows + kPrefillRows - 1) / kPrefillRows;
-  const int seg = blockIdx.x / nblk, rblk = blockIdx.x % nblk;
+  // Blocks of one (sequence, KV head) read the same pages: give them
+  // consecutive slots of one XCD (workgroups are dealt to the 8 XCDs
+  // round-robin) so the span is fetched into one L2.
+  int bid = blockIdx.x;
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int nblk = (a.rows + ROWS - 1) / ROWS;
+  const int seg = bid / nblk, rblk = bid % nblk;
   const int b = seg / g.hk, kh = seg % g.hk;
   if (b >= a.batch) return;
   const int L = a.seq_lens[b];
   const int width = a.widths ? a.widths[b] : a.nq;
 
-  // ---- the wave's 32 query rows: row = 128*rblk + 32*wv + 16*rb + col
+  // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];
-  KT qv[RB][KB];
-  float qs[RB][NG];
+  OT qv[RB][KB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int row = rblk * kPrefillRows + wv * 32 + rb * 16 + col;
+    const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
     const bool valid = row < a.rows;
     const int rowv = valid ? row : 0;  // rows past the block load row 0, zeroed below
     const int qi = rowv / a.gqa, h = kh * a.gqa + rowv % a.gqa;
     const bool live = valid && qi < width;
     const int pos = a.q_pos ? a.q_pos[(int64_t)b * a.nq + qi] : L - width + qi;
     lim[rb] = live ? min(pos, L - 1) : -1;
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) qs[rb][gi] = 0.0f;
     const uint16_t *qrow = a.q + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -121,37 +125,28 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (!valid || d0 + e >= g.dim) e8[e] = 0;
-      if constexpr (QUANT || FK == 1) {
+      if constexpr (F16) {
         h8 v;
-        float sum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const _Float16 hv = (_Float16)bits_to_float(e8[e], g.float_kind);
-          v[e] = hv;
-          sum += (float)hv;
-        }
-        if constexpr (QUANT) qs[rb][(32 * kb) / G] += sum;
-        qv[rb][kb] = __builtin_bit_cast(KT, v);
+        for (int e = 0; e < 8; ++e) v[e] = (_Float16)bits_to_float(e8[e], g.float_kind);
+        qv[rb][kb] = v;
       } else {
         u4 packed = {(uint32_t)e8[0] | ((uint32_t)e8[1] << 16), (uint32_t)e8[2] | ((uint32_t)e8[3] << 16),
                      (uint32_t)e8[4] | ((uint32_t)e8[5] << 16), (uint32_t)e8[6] | ((uint32_t)e8[7] << 16)};
-        qv[rb][kb] = __builtin_bit_cast(KT, packed);
-      }
-    }
-    if constexpr (QUANT) {
-#pragma unroll
-      for (int gi = 0; gi < NG; ++gi) {
-        qs[rb][gi] += __shfl_xor(qs[rb][gi], 16, 64);
-        qs[rb][gi] += __shfl_xor(qs[rb][gi], 32, 64);
+        qv[rb][kb] = __builtin_bit_cast(OT, packed);
       }
     }
   }
 
   // ---- the block's visible span: tokens up to the largest limit; tiles
-  // below the smallest live limit need no per-token mask
+  // below the smallest live limit are seen whole by every live row
   {
-    int hi = max(lim[0], lim[1]);
-    int lo = min(lim[0] < 0 ? 0x7FFFFFFF : lim[0], lim[1] < 0 ? 0x7FFFFFFF : lim[1]);
+    int hi = lim[0], lo = lim[0] < 0 ? 0x7FFFFFFF : lim[0];
+#pragma unroll
+    for (int rb = 1; rb < RB; ++rb) {
+      hi = max(hi, lim[rb]);
+      lo = min(lo, lim[rb] < 0 ? 0x7FFFFFFF : lim[rb]);
+    }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       hi = max(hi, __shfl_xor(hi, o, 64));
@@ -172,70 +167,113 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   tmax = __builtin_amdgcn_readfirstlane(tmax);
   tmin = __builtin_amdgcn_readfirstlane(tmin);
   const int ntiles = tmax >= 0 ? tmax / PKV_TILE + 1 : 0;
-  const int clear_tiles = tmin == 0x7FFFFFFF ? 0 : (tmin + 1) / PKV_TILE;  // tiles every live row sees whole
+  const int clear_tiles = tmin == 0x7FFFFFFF ? 0 : (tmin + 1) / PKV_TILE;
   const int nstages = (ntiles + kStageTiles - 1) / kStageTiles;
   const int tpp_shift = __builtin_ctz(g.page / PKV_TILE);
   const int tpp_mask = (1 << tpp_shift) - 1;
 
-  // Stage s, tile s*4 + wv is DMA'd by wave wv into slot wv of stage buffer
-  // s&1; absent tiles (past the span, unmapped pages) read head block kh of
-  // page 0 so every wave issues the same DMA count, and are flagged invalid.
-  auto issue = [&](int s, uint8_t (&stage)[kStageTiles][SLOT], int buf) __attribute__((always_inline)) {
+  // ---- raw tile in flight: wave wv owns tile 4s + wv of stage s
+  uint32_t rk[LW], rv[LW];
+  uint32_t rkm[QUANT ? NG : 1], rvm[QUANT ? 4 * NG : 4];
+  int r_ok = 0, r_t = 0;
+  auto fetch = [&](int s) __attribute__((always_inline)) {
     const int t = s * kStageTiles + wv;
-    int id = 0, tip = 0, ok = 0;
+    int id = -1, tip = 0;
     if (t < ntiles) {
       const int p = t >> tpp_shift;
       const int pid = p < a.max_pages ? ((const_i32 *)(uintptr_t)a.table)[(int64_t)b * a.max_pages + p] : -1;
       if (pid >= 0 && pid < a.num_pages) {
         id = pid;
         tip = t & tpp_mask;
-        ok = 1;
       }
     }
-    if (lane == 0) s_valid[buf][wv] = ok;
-    const uint8_t *head = a.pool + (int64_t)id * g.page_bytes + (int64_t)kh * g.head_bytes;
-    const int64_t off = (int64_t)tip * g.tile_bytes;
-    const uint8_t *kt = head + off, *vt = head + g.v_offset + off;
-    uint8_t *dst = stage[wv];
-    if constexpr (C::CS == 16) {
+    r_ok = id >= 0;
+    r_t = t;
+    if (r_ok) {
+      const uint8_t *head = a.pool + (int64_t)id * g.page_bytes + (int64_t)kh * g.head_bytes;
+      const int64_t off = (int64_t)tip * g.tile_bytes;
+      load_payload<C>(rk, head + off, lane);
+      load_payload<C>(rv, head + g.v_offset + off, lane);
+      if constexpr (QUANT) {
+        const uint8_t *km = head + g.kmeta_offset + (int64_t)((tip * PKV_TILE + col) * NG) * 4;
+        if constexpr (NG == 1) {
+          rkm[0] = *(const uint32_t *)km;
+        } else if constexpr (NG == 2) {
+          const u2 x = *(const u2 *)km;
+          rkm[0] = x.x; rkm[1] = x.y;
+        } else {
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c) dma16(kt + c * 1024 + lane * 16, dst + c * 1024);
-#pragma unroll
-      for (int c = 0; c < C::NCH; ++c) dma16(vt + c * 1024 + lane * 16, dst + KP + c * 1024);
-    } else {
-      dma4(kt + lane * 8, dst);
-      dma4(kt + lane * 8 + 4, dst + 256);
-      dma4(vt + lane * 8, dst + KP);
-      dma4(vt + lane * 8 + 4, dst + KP + 256);
-    }
-    if constexpr (QUANT) {
-      const int base = tip * PKV_TILE * NG;
-#pragma unroll
-      for (int m = 0; m < 32 * NG; m += 64) {
-        const int idx = m + lane;
-        if (idx < 32 * NG) {
-          const uint8_t *src = idx < 16 * NG ? head + g.kmeta_offset + (int64_t)(base + idx) * 4
-                                             : head + g.vmeta_offset + (int64_t)(base + idx - 16 * NG) * 4;
-          dma4(src, dst + 2 * KP + m * 4);
+          for (int i = 0; i < NG; i += 4) {
+            const u4 x = *(const u4 *)(km + i * 4);
+            rkm[i] = x.x; rkm[i + 1] = x.y; rkm[i + 2] = x.z; rkm[i + 3] = x.w;
+          }
         }
+        load_meta<C>(rvm, head + g.vmeta_offset + (int64_t)((tip * PKV_TILE + 4 * jj) * NG) * 4);
       }
-    }
-  };
-  // A lane's K or V payload and metadata words of a staged tile.
-  auto lds_payload = [&](uint32_t (&w)[C::LW], const uint8_t *p) __attribute__((always_inline)) {
-    if constexpr (C::CS == 16) {
-#pragma unroll
-      for (int c = 0; c < C::NCH; ++c) {
-        const u4 x = *(const u4 *)(p + c * 1024 + lane * 16);
-        w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
-      }
-    } else {
-      w[0] = *(const uint32_t *)(p + lane * 4);
-      w[1] = *(const uint32_t *)(p + 256 + lane * 4);
     }
   };
 
-  float m[RB], lsum[RB], corr[RB][NG], osum[RB][NG];
+  // ---- convert the raw tile into slot wv of a stage image
+  auto convert = [&](uint16_t *img) __attribute__((always_inline)) {
+    const int tok0 = r_t * PKV_TILE;
+    const bool whole = r_ok && tok0 + PKV_TILE <= L;  // uniform
+    const bool kvalid = r_ok && tok0 + col < L;
+    bool vvalid[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vvalid[e] = r_ok && tok0 + 4 * jj + e < L;
+    uint16_t *kdst = img + wv * I::KTILE + col * I::KROW + 8 * jj;
+    uint16_t *vdst = img + I::K_ELEMS + col * I::VROW + 32 * (wv >> 1) + 8 * jj + 4 * (wv & 1);
+    if constexpr (QUANT) {
+      // absent tokens: scale = bias = 0 -> exact zeros
+      uint32_t km[NG], vm[4 * NG];
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) km[gi] = whole || kvalid ? rkm[gi] : 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) vm[e * NG + gi] = whole || vvalid[e] ? rvm[e * NG + gi] : 0u;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const h2 sb = __builtin_bit_cast(h2, km[(32 * kb) / G]);
+        const h8 sc = {sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x};
+        const h8 bi = {sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y};
+        const h8 c = Conv<BITS>::template kop<LW>(rk, kb);
+        const h8 v = __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi);
+        *(u4 *)(kdst + 32 * kb) = __builtin_bit_cast(u4, v);
+      }
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const int gi = (16 * n) / G;
+        h4 sc, bi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const h2 sb = __builtin_bit_cast(h2, vm[e * NG + gi]);
+          sc[e] = sb.x;
+          bi[e] = sb.y;
+        }
+        const h4 c = Conv<BITS>::template vop<LW>(rv, n);
+        const h4 v = __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi);
+        *(u2 *)(vdst + 16 * n * I::VROW) = __builtin_bit_cast(u2, v);
+      }
+    } else {
+      const uint32_t kmask = whole || kvalid ? 0xFFFFFFFFu : 0u;
+      const uint32_t vmask0 = whole ? 0xFFFFFFFFu : (vvalid[0] ? 0xFFFFu : 0u) | (vvalid[1] ? 0xFFFF0000u : 0u);
+      const uint32_t vmask1 = whole ? 0xFFFFFFFFu : (vvalid[2] ? 0xFFFFu : 0u) | (vvalid[3] ? 0xFFFF0000u : 0u);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const u4 v = {rk[4 * kb] & kmask, rk[4 * kb + 1] & kmask, rk[4 * kb + 2] & kmask, rk[4 * kb + 3] & kmask};
+        *(u4 *)(kdst + 32 * kb) = v;
+      }
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const u2 v = {rv[2 * n] & vmask0, rv[2 * n + 1] & vmask1};
+        *(u2 *)(vdst + 16 * n * I::VROW) = v;
+      }
+    }
+    if (lane == 0) s_valid[(r_t / kStageTiles) & 1][wv] = r_ok;
+  };
+
+  float m[RB], lsum[RB];
   f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -243,68 +281,62 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
     lsum[rb] = 0.0f;
 #pragma unroll
     for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] = 0.0f; osum[rb][gi] = 0.0f; }
   }
+  const float c_log2 = a.scale_log2;
 
-  // one staged tile: scores, softmax, PV for the wave's 32 rows
-  auto tile = [&](const uint8_t *slot, int t) __attribute__((always_inline)) {
-    uint32_t kw[C::LW];
-    lds_payload(kw, slot);
-    f4 acc[RB][NG];
+  // ---- one step: tiles 4s + 2pr and 4s + 2pr + 1 of stage image img
+  auto step = [&](const uint16_t *img, int s, int pr, int buf) __attribute__((always_inline)) {
+    const int ta = s * kStageTiles + 2 * pr;
+    const bool oka = s_valid[buf][2 * pr] != 0;
+    const bool okb = ta + 1 < ntiles && s_valid[buf][2 * pr + 1] != 0;
+    const bool fast = __builtin_amdgcn_readfirstlane(oka && okb && ta + 1 < clear_tiles);
+    f4 S[2][RB];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int gi = 0; gi < NG; ++gi) acc[rb][gi] = f4{0, 0, 0, 0};
+      for (int rb = 0; rb < RB; ++rb) S[i][rb] = f4{0, 0, 0, 0};
+    const uint16_t *kbase = img + 2 * pr * I::KTILE + col * I::KROW + 8 * jj;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      KT kop;
-      if constexpr (QUANT) {
-        kop = Conv<BITS>::template kop<C::LW>(kw, kb);
-      } else {
-        u4 r = {kw[4 * kb], kw[4 * kb + 1], kw[4 * kb + 2], kw[4 * kb + 3]};
-        kop = __builtin_bit_cast(KT, r);
-      }
-      const int gi = QUANT ? (32 * kb) / G : 0;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) acc[rb][gi] = FO::qk(kop, qv[rb][kb], acc[rb][gi]);
+      for (int i = 0; i < 2; ++i) {
+        const OT kop = __builtin_bit_cast(OT, *(const u4 *)(kbase + i * I::KTILE + 32 * kb));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          if constexpr (F16)
+            S[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qv[rb][kb], S[i][rb], 0, 0, 0);
+          else
+            S[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qv[rb][kb], S[i][rb], 0, 0, 0);
+        }
+      }
     }
-    uint32_t km[C::MW], vm[C::MW];
-    if constexpr (QUANT) {
-      load_meta<C>(km, slot + 2 * KP + 4 * jj * NG * 4);
-      load_meta<C>(vm, slot + 2 * KP + 16 * NG * 4 + 4 * jj * NG * 4);
-    }
-    const int tok0 = t * PKV_TILE + 4 * jj;
-    const bool clear = t < clear_tiles;  // uniform: every live row sees the whole tile
-    float s[RB][4];
-    bool vis[RB][4];
+    float v[RB][8];
     bool need = false;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v;
-        if constexpr (QUANT) {
-          v = 0.0f;
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int gi = 0; gi < NG; ++gi) {
-            const uint32_t word = km[r * NG + gi];
-            const float ks = f16_bits_to_f32(word);
-            const float kbias = f16_bits_to_f32(word >> 16) - 1024.0f * ks;
-            v += ks * acc[rb][gi][r] + qs[rb][gi] * kbias;
+        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = S[i][rb][r] * c_log2;
+      if (!fast) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = (ta + i) * PKV_TILE + 4 * jj + r;
+            const bool vis = (i ? okb : oka) && tok <= lim[rb];
+            v[rb][4 * i + r] = vis ? v[rb][4 * i + r] : -INFINITY;
           }
-        } else {
-          v = acc[rb][0][r];
-        }
-        vis[rb][r] = clear ? lim[rb] >= 0 : tok0 + r <= lim[rb];
-        v = vis[rb][r] ? v * a.scale_log2 : -INFINITY;
-        s[rb][r] = v;
-        need |= v > m[rb] + kTau;
       }
+      const float mx = fmaxf(fmaxf(fmaxf(v[rb][0], v[rb][1]), fmaxf(v[rb][2], v[rb][3])),
+                             fmaxf(fmaxf(v[rb][4], v[rb][5]), fmaxf(v[rb][6], v[rb][7])));
+      need |= mx > m[rb] + kTau;
+    }
     if (__any(need)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        float tm = fmaxf(fmaxf(s[rb][0], s[rb][1]), fmaxf(s[rb][2], s[rb][3]));
+        float tm = fmaxf(fmaxf(fmaxf(v[rb][0], v[rb][1]), fmaxf(v[rb][2], v[rb][3])),
+                         fmaxf(fmaxf(v[rb][4], v[rb][5]), fmaxf(v[rb][6], v[rb][7])));
         tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
         tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
         const float mn = fmaxf(m[rb], tm);
@@ -312,78 +344,61 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
         m[rb] = mn;
         lsum[rb] *= alpha;
 #pragma unroll
-        for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] *= alpha; osum[rb][gi] *= alpha; }
-#pragma unroll
         for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
       }
     }
-    VT pop[RB][NG];
+    OT P[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      float p[4];
+      float p[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = vis[rb][r] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
-      lsum[rb] += (p[0] + p[1]) + (p[2] + p[3]);
-      if constexpr (QUANT) {
-#pragma unroll
-        for (int gi = 0; gi < NG; ++gi) {
-          h4 pv;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t word = vm[r * NG + gi];
-            // absent tokens contribute exact zeros whatever their metadata holds
-            const _Float16 ps = (_Float16)(p[r] * f16_bits_to_f32(word));
-            pv[r] = vis[rb][r] ? ps : (_Float16)0.0f;
-            corr[rb][gi] += vis[rb][r] ? p[r] * f16_bits_to_f32(word >> 16) : 0.0f;
-            osum[rb][gi] += (float)pv[r];
-          }
-          pop[rb][gi] = pv;
-        }
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(v[rb][e] - m[rb]);
+        if (!fast) p[e] = v[rb][e] == -INFINITY ? 0.0f : p[e];
+      }
+      lsum[rb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      if constexpr (F16) {
+        P[rb] = h8{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+                   (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
       } else {
-        pop[rb][0] = FO::pack_p(p[0], p[1], p[2], p[3]);
+        P[rb] = b8{(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3],
+                   (__bf16)p[4], (__bf16)p[5], (__bf16)p[6], (__bf16)p[7]};
       }
     }
-    uint32_t vw[C::LW];
-    lds_payload(vw, slot + KP);
+    const uint16_t *vbase = img + I::K_ELEMS + col * I::VROW + 32 * pr + 8 * jj;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      VT vop;
-      if constexpr (QUANT) {
-        vop = Conv<BITS>::template vop<C::LW>(vw, n);
-      } else {
-        u2 r = {vw[2 * n], vw[2 * n + 1]};
-        vop = __builtin_bit_cast(VT, r);
-      }
-      const int gi = QUANT ? (16 * n) / G : 0;
+      const OT vop = __builtin_bit_cast(OT, *(const u4 *)(vbase + 16 * n * I::VROW));
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) O[rb][n] = FO::pv(vop, pop[rb][gi], O[rb][n]);
+      for (int rb = 0; rb < RB; ++rb) {
+        if constexpr (F16)
+          O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, P[rb], O[rb][n], 0, 0, 0);
+        else
+          O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, P[rb], O[rb][n], 0, 0, 0);
+      }
     }
   };
 
-  // ---- stream the span: DMA stage s+1 while computing stage s
-  auto run_stage = [&](int s, uint8_t (&cur)[kStageTiles][SLOT], uint8_t (&nxt)[kStageTiles][SLOT],
-                       int buf) __attribute__((always_inline)) {
+  // ---- stream the span.  Iteration s computes stage s from image s&1,
+  // converts the tile of stage s+1 (loaded during stage s-1) into image
+  // (s+1)&1 -- last read in iteration s-1, before its barrier -- and issues
+  // the loads of stage s+2.
+  if (nstages > 0) {
+    fetch(0);
+    convert(stage[0]);
+    if (nstages > 1) fetch(1);
+  }
+  lds_barrier();
+  for (int s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    const uint16_t *img = stage[buf];
+    step(img, s, 0, buf);
+    if (s * kStageTiles + 2 < ntiles) step(img, s, 1, buf);
     if (s + 1 < nstages) {
-      issue(s + 1, nxt, buf ^ 1);
-      stage_barrier<LPT>();  // every wave's DMAs of stage s have landed (stage s+1's are younger)
-    } else {
-      stage_barrier<0>();
+      convert(stage[buf ^ 1]);
+      if (s + 2 < nstages) fetch(s + 2);
     }
-    if (s < 0) return;
-#pragma unroll 1
-    for (int j = 0; j < kStageTiles; ++j) {
-      const int t = s * kStageTiles + j;
-      if (t >= ntiles) break;
-      if (!__builtin_amdgcn_readfirstlane(s_valid[buf][j])) continue;
-      tile(cur[j], t);
-    }
-    stage_barrier<63>();  // every wave is done reading this buffer: free for stage s+2
-  };
-  // rotated so that every DMA is issued from inside the loop (stage s lives
-  // in buffer s&1; the first pass only issues stage 0)
-  for (int s = -1; s < nstages; s += 2) {
-    run_stage(s, stage1, stage0, 1);
-    if (s + 1 < nstages) run_stage(s + 1, stage0, stage1, 0);
+    lds_barrier();
   }
 
   // ---- epilogue: fold the 4 jj lanes of a column, normalise, write
@@ -391,30 +406,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   for (int rb = 0; rb < RB; ++rb) {
     lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
     lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-      corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
-      corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
-      osum[rb][gi] += __shfl_xor(osum[rb][gi], 16, 64);
-      osum[rb][gi] += __shfl_xor(osum[rb][gi], 32, 64);
-    }
-    const int row = rblk * kPrefillRows + wv * 32 + rb * 16 + col;
+    const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
     if (row >= a.rows) continue;
     const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-    const float inv = 1.0f / fmaxf(lsum[rb], 1e-20f);
+    // dead rows (past the chunk's width) ran the unmasked steps: write 0
+    const float inv = lim[rb] < 0 ? 0.0f : 1.0f / fmaxf(lsum[rb], 1e-20f);
     uint16_t *o = a.out + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       float v4[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = O[rb][n][r];
-        if constexpr (QUANT) {
-          const int gi = (16 * n) / G;
-          v += corr[rb][gi] - 1024.0f * osum[rb][gi];
-        }
-        v4[r] = v * inv;
-      }
+      for (int r = 0; r < 4; ++r) v4[r] = lim[rb] < 0 ? 0.0f : O[rb][n][r] * inv;
       const int d = 16 * n + 4 * jj;
       if ((g.dim & 3) == 0 && d + 4 <= g.dim) {
         u2 packed = {(uint32_t)float_to_bits(v4[0], g.float_kind) |
@@ -455,7 +457,8 @@ static PrefillKernel select_prefill(const Geo &g) {
 hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a) {
   const PrefillKernel k = select_prefill(a.g);
   if (!k) return hipErrorInvalidValue;
-  const int64_t blocks = (int64_t)a.batch * a.g.hk * ((a.rows + kPrefillRows - 1) / kPrefillRows);
+  const int rows_per_block = prefill_rows(a.g.dp);
+  const int64_t blocks = (int64_t)a.batch * a.g.hk * ((a.rows + rows_per_block - 1) / rows_per_block);
   if (blocks == 0) return hipSuccess;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(64 * kPrefillWaves), 0, stream, a);

@@ -33,6 +33,7 @@ class Workload:
     outlier_fraction: float = 0.0
     outlier_scale: float = 8.0
     arena_pages: int = 0           # 0 = exactly the pages needed (+ spare)
+    fixed_chunk: bool = False      # every step re-appends the same chunk (fixed shape)
     seed: int = 0
     description: str = ""
 
@@ -57,7 +58,7 @@ CONFIGS = {
                                "shared prefix"),
     "c5": Workload("c5", batch=4, heads=32, kv_heads=8, head_dim=128, page_tokens=16, bits=8,
                    group_size=64, num_queries=512, append_tokens=512, lengths=(4096,) * 4,
-                   seed=4,
+                   fixed_chunk=True, seed=4,
                    description="int8 G64 chunked prefill: 512-token causal query chunk per "
                                "sequence over a 4096-token paged prefix plus the chunk, B4 "
                                "H32/HK8 D128 P16"),

@@ -157,6 +157,20 @@ def test_workload_waves():
     assert bench.workload_waves(workloads.get("c2"), [5000] * 32) == 0   # device capacity
 
 
+def test_prefill_flops_match_the_causal_count():
+    """C5 flops: the closed form 4*D*H*B*(512*4096 + 512*513/2) and a brute-force
+    count of (query, visible token) pairs on a small chunk."""
+    import bench
+
+    c5 = workloads.get("c5")
+    assert bench.is_prefill(c5) and not bench.is_prefill(workloads.get("c4"))
+    assert bench.attention_flops(c5, [4608] * 4) == 4 * 128 * 32 * 4 * (512 * 4096 + 512 * 513 // 2)
+    small = workloads.get("c5", batch=2, num_queries=7, heads=2, kv_heads=1, head_dim=3)
+    lengths = [20, 9]
+    pairs = sum(1 for n in lengths for q in range(7) for t in range(n) if t <= n - 7 + q)
+    assert bench.attention_flops(small, lengths) == 4 * 3 * 2 * pairs
+
+
 def test_bench_bytes_match_the_configs():
     """Algorithmic bytes of bench.py against the per-config figures (C2 at E[L], C3 exact)."""
     import bench
