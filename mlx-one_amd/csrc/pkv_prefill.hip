@@ -61,10 +61,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// Page-table reads through the constant address space: uniform indices give
-// scalar loads.
-typedef const __attribute__((address_space(4))) int32_t const_i32;
-
 template <int BITS, int DP, int G, int FK>
 __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   constexpr int RB = prefill_rb(DP);
@@ -76,7 +72,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   using I = StageImage<DP>;
   typedef typename std::conditional<F16, h8, b8>::type OT;  // 8-element MFMA operand
 
-  __shared__ int s_valid[2][kStageTiles];
+  __shared__ __attribute__((aligned(16))) int s_valid[2][kStageTiles];
   __shared__ int s_lim[2][kPrefillWaves];
   __shared__ __attribute__((aligned(16))) uint16_t stage[2][I::ELEMS];
 
@@ -125,16 +121,16 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (!valid || d0 + e >= g.dim) e8[e] = 0;
-      if constexpr (F16) {
-        h8 v;
+      // queries pre-scaled by scale*log2(e): scores leave the MFMA in the
+      // exp2 domain
+      OT v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (_Float16)bits_to_float(e8[e], g.float_kind);
-        qv[rb][kb] = v;
-      } else {
-        u4 packed = {(uint32_t)e8[0] | ((uint32_t)e8[1] << 16), (uint32_t)e8[2] | ((uint32_t)e8[3] << 16),
-                     (uint32_t)e8[4] | ((uint32_t)e8[5] << 16), (uint32_t)e8[6] | ((uint32_t)e8[7] << 16)};
-        qv[rb][kb] = __builtin_bit_cast(OT, packed);
+      for (int e = 0; e < 8; ++e) {
+        const float x = bits_to_float(e8[e], g.float_kind) * a.scale_log2;
+        if constexpr (F16) v[e] = (_Float16)x;
+        else v[e] = (__bf16)x;
       }
+      qv[rb][kb] = v;
     }
   }
 
@@ -175,25 +171,43 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   // ---- raw tile in flight: wave wv owns tile 4s + wv of stage s
   uint32_t rk[LW], rv[LW];
   uint32_t rkm[QUANT ? NG : 1], rvm[QUANT ? 4 * NG : 4];
-  int r_ok = 0, r_t = 0;
-  auto fetch = [&](int s) __attribute__((always_inline)) {
-    const int t = s * kStageTiles + wv;
-    int id = -1, tip = 0;
+  int k_ok = 0, k_t = 0, v_ok = 0, v_t = 0;  // tile whose K (V) half sits in rk (rv)
+  // Page ids of the sequence, 64 per window: lane i holds entry wbase + i;
+  // the next window is loaded 64 pages ahead, so a lookup is one readlane.
+  const int32_t *trow = a.table + (int64_t)b * a.max_pages;
+  auto load_ids = [&](int base) __attribute__((always_inline)) {
+    const int p = base + lane;
+    return p < a.max_pages ? trow[p] : -1;
+  };
+  int wbase = 0;
+  int pwin = load_ids(0), pnext = load_ids(64);
+  // tile 4s + wv of stage s -> (present, tile, head block, tile offset)
+  auto locate = [&](int s, int &ok, int &t, const uint8_t *&head, int &tip) __attribute__((always_inline)) {
+    t = s * kStageTiles + wv;
+    int id = -1;
+    tip = 0;
     if (t < ntiles) {
       const int p = t >> tpp_shift;
-      const int pid = p < a.max_pages ? ((const_i32 *)(uintptr_t)a.table)[(int64_t)b * a.max_pages + p] : -1;
+      if (p >= wbase + 64) {  // pages advance at most 4 per stage
+        pwin = pnext;
+        wbase += 64;
+        pnext = load_ids(wbase + 64);
+      }
+      const int pid = __builtin_amdgcn_readlane(pwin, p - wbase);
       if (pid >= 0 && pid < a.num_pages) {
         id = pid;
         tip = t & tpp_mask;
       }
     }
-    r_ok = id >= 0;
-    r_t = t;
-    if (r_ok) {
-      const uint8_t *head = a.pool + (int64_t)id * g.page_bytes + (int64_t)kh * g.head_bytes;
-      const int64_t off = (int64_t)tip * g.tile_bytes;
-      load_payload<C>(rk, head + off, lane);
-      load_payload<C>(rv, head + g.v_offset + off, lane);
+    ok = id >= 0;
+    head = a.pool + (int64_t)(ok ? id : 0) * g.page_bytes + (int64_t)kh * g.head_bytes;
+  };
+  auto fetch_k = [&](int s) __attribute__((always_inline)) {
+    const uint8_t *head;
+    int tip;
+    locate(s, k_ok, k_t, head, tip);
+    if (k_ok) {
+      load_payload<C>(rk, head + (int64_t)tip * g.tile_bytes, lane);
       if constexpr (QUANT) {
         const uint8_t *km = head + g.kmeta_offset + (int64_t)((tip * PKV_TILE + col) * NG) * 4;
         if constexpr (NG == 1) {
@@ -208,14 +222,26 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
             rkm[i] = x.x; rkm[i + 1] = x.y; rkm[i + 2] = x.z; rkm[i + 3] = x.w;
           }
         }
-        load_meta<C>(rvm, head + g.vmeta_offset + (int64_t)((tip * PKV_TILE + 4 * jj) * NG) * 4);
       }
     }
   };
+  auto fetch_v = [&](int s) __attribute__((always_inline)) {
+    const uint8_t *head;
+    int tip;
+    locate(s, v_ok, v_t, head, tip);
+    if (v_ok) {
+      load_payload<C>(rv, head + g.v_offset + (int64_t)tip * g.tile_bytes, lane);
+      if constexpr (QUANT)
+        load_meta<C>(rvm, head + g.vmeta_offset + (int64_t)((tip * PKV_TILE + 4 * jj) * NG) * 4);
+    }
+  };
 
-  // ---- convert the raw tile into slot wv of a stage image
-  auto convert = [&](uint16_t *img) __attribute__((always_inline)) {
-    const int tok0 = r_t * PKV_TILE;
+  // ---- convert the raw tile into slot wv of a stage image (K half, then V
+  // half: each is scheduled against one step's MFMAs)
+  auto convert = [&](int dst, bool k_half) __attribute__((always_inline)) {
+    uint16_t *img = stage[dst];
+    const int r_ok = k_half ? k_ok : v_ok;
+    const int tok0 = (k_half ? k_t : v_t) * PKV_TILE;
     const bool whole = r_ok && tok0 + PKV_TILE <= L;  // uniform
     const bool kvalid = r_ok && tok0 + col < L;
     bool vvalid[4];
@@ -233,7 +259,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) vm[e * NG + gi] = whole || vvalid[e] ? rvm[e * NG + gi] : 0u;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+      for (int kb = 0; kb < (k_half ? KB : 0); ++kb) {
         const h2 sb = __builtin_bit_cast(h2, km[(32 * kb) / G]);
         const h8 sc = {sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x};
         const h8 bi = {sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y};
@@ -242,7 +268,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
         *(u4 *)(kdst + 32 * kb) = __builtin_bit_cast(u4, v);
       }
 #pragma unroll
-      for (int n = 0; n < NB; ++n) {
+      for (int n = 0; n < (k_half ? 0 : NB); ++n) {
         const int gi = (16 * n) / G;
         h4 sc, bi;
 #pragma unroll
@@ -260,17 +286,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
       const uint32_t vmask0 = whole ? 0xFFFFFFFFu : (vvalid[0] ? 0xFFFFu : 0u) | (vvalid[1] ? 0xFFFF0000u : 0u);
       const uint32_t vmask1 = whole ? 0xFFFFFFFFu : (vvalid[2] ? 0xFFFFu : 0u) | (vvalid[3] ? 0xFFFF0000u : 0u);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+      for (int kb = 0; kb < (k_half ? KB : 0); ++kb) {
         const u4 v = {rk[4 * kb] & kmask, rk[4 * kb + 1] & kmask, rk[4 * kb + 2] & kmask, rk[4 * kb + 3] & kmask};
         *(u4 *)(kdst + 32 * kb) = v;
       }
 #pragma unroll
-      for (int n = 0; n < NB; ++n) {
+      for (int n = 0; n < (k_half ? 0 : NB); ++n) {
         const u2 v = {rv[2 * n] & vmask0, rv[2 * n + 1] & vmask1};
         *(u2 *)(vdst + 16 * n * I::VROW) = v;
       }
     }
-    if (lane == 0) s_valid[(r_t / kStageTiles) & 1][wv] = r_ok;
+    if (!k_half && lane == 0) s_valid[dst][wv] = r_ok;
   };
 
   float m[RB], lsum[RB];
@@ -282,19 +308,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
 #pragma unroll
     for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
   }
-  const float c_log2 = a.scale_log2;
 
-  // ---- one step: tiles 4s + 2pr and 4s + 2pr + 1 of stage image img
-  auto step = [&](const uint16_t *img, int s, int pr, int buf) __attribute__((always_inline)) {
-    const int ta = s * kStageTiles + 2 * pr;
-    const bool oka = s_valid[buf][2 * pr] != 0;
-    const bool okb = ta + 1 < ntiles && s_valid[buf][2 * pr + 1] != 0;
-    const bool fast = __builtin_amdgcn_readfirstlane(oka && okb && ta + 1 < clear_tiles);
-    f4 S[2][RB];
+  // max of 8 values (v_maximum3_f32: no NaN canonicalisation)
+  auto max8 = [](const float (&x)[8]) __attribute__((always_inline)) {
+    const float a3 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[0], x[1]), x[2]);
+    const float b3 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[3], x[4]), x[5]);
+    const float c3 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[6], x[7]), a3);
+    return __builtin_elementwise_maximum(b3, c3);
+  };
+
+  // ---- one step covers tiles 4s + 2pr and 4s + 2pr + 1 of a stage image.
+  // S^T = K.Q^T for both tiles.  The accumulators start at -mb (the running
+  // max, 0 before any token is seen), so the MFMAs leave v = s - mb.
+  auto qk = [&](const uint16_t *img, int pr, f4 (&S)[2][RB], float (&mb)[RB]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int rb = 0; rb < RB; ++rb) {
+      mb[rb] = m[rb] == -INFINITY ? 0.0f : m[rb];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) S[i][rb] = f4{0, 0, 0, 0};
+      for (int i = 0; i < 2; ++i) S[i][rb] = f4{-mb[rb], -mb[rb], -mb[rb], -mb[rb]};
+    }
     const uint16_t *kbase = img + 2 * pr * I::KTILE + col * I::KROW + 8 * jj;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -310,14 +342,23 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
         }
       }
     }
-    float v[RB][8];
+  };
+  // Masks (steps not seen whole by every live row), then the lazy rescale:
+  // only when a score exceeds the running max by more than kTau.
+  auto scores = [&](const f4 (&S)[2][RB], const float (&mb)[RB], int s, int pr, int okv,
+                    float (&v)[RB][8]) __attribute__((always_inline)) {
+    const int ta = s * kStageTiles + 2 * pr;
+    const bool oka = (okv >> (2 * pr)) & 1;
+    const bool okb = ta + 1 < ntiles && ((okv >> (2 * pr + 1)) & 1);
+    const bool fast = oka && okb && ta + 1 < clear_tiles;
+    float mx[RB];
     bool need = false;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = S[i][rb][r] * c_log2;
+        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = S[i][rb][r];
       if (!fast) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -328,34 +369,37 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
             v[rb][4 * i + r] = vis ? v[rb][4 * i + r] : -INFINITY;
           }
       }
-      const float mx = fmaxf(fmaxf(fmaxf(v[rb][0], v[rb][1]), fmaxf(v[rb][2], v[rb][3])),
-                             fmaxf(fmaxf(v[rb][4], v[rb][5]), fmaxf(v[rb][6], v[rb][7])));
-      need |= mx > m[rb] + kTau;
+      mx[rb] = max8(v[rb]);
+      // before any token is seen every finite score resets the max
+      need |= mx[rb] > (m[rb] == -INFINITY ? -INFINITY : kTau);
     }
     if (__any(need)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        float tm = fmaxf(fmaxf(fmaxf(v[rb][0], v[rb][1]), fmaxf(v[rb][2], v[rb][3])),
-                         fmaxf(fmaxf(v[rb][4], v[rb][5]), fmaxf(v[rb][6], v[rb][7])));
-        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-        const float mn = fmaxf(m[rb], tm);
-        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[rb] - mn);
-        m[rb] = mn;
-        lsum[rb] *= alpha;
+        float tm = mx[rb];
+        tm = __builtin_elementwise_maximum(tm, __shfl_xor(tm, 16, 64));
+        tm = __builtin_elementwise_maximum(tm, __shfl_xor(tm, 32, 64));
+        const float mn = fmaxf(m[rb], tm + mb[rb]);
+        if (mn != -INFINITY && mn != m[rb]) {
+          const float shift = mn - mb[rb];
+          const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);  // 0 when m was -inf
 #pragma unroll
-        for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
+          for (int e = 0; e < 8; ++e) v[rb][e] -= shift;
+          m[rb] = mn;
+          lsum[rb] *= alpha;
+#pragma unroll
+          for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
+        }
       }
     }
-    OT P[RB];
+  };
+  // P = exp2(v) (masked: exp2(-inf) = 0), row sums, packed operand
+  auto probs = [&](const float (&v)[RB][8], OT (&P)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float p[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(v[rb][e] - m[rb]);
-        if (!fast) p[e] = v[rb][e] == -INFINITY ? 0.0f : p[e];
-      }
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(v[rb][e]);
       lsum[rb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       if constexpr (F16) {
         P[rb] = h8{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
@@ -365,6 +409,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
                    (__bf16)p[4], (__bf16)p[5], (__bf16)p[6], (__bf16)p[7]};
       }
     }
+  };
+  // O^T += V^T.P^T over the step's 32 tokens
+  auto pv = [&](const uint16_t *img, int pr, const OT (&P)[RB]) __attribute__((always_inline)) {
     const uint16_t *vbase = img + I::K_ELEMS + col * I::VROW + 32 * pr + 8 * jj;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
@@ -382,22 +429,45 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   // ---- stream the span.  Iteration s computes stage s from image s&1,
   // converts the tile of stage s+1 (loaded during stage s-1) into image
   // (s+1)&1 -- last read in iteration s-1, before its barrier -- and issues
-  // the loads of stage s+2.
+  // the loads of stage s+2.  Within a stage the second step's QK MFMAs are
+  // issued before the first step's exponentials and the conversion halves
+  // sit beside the PV MFMAs, so that the MFMA and VALU pipes overlap.  Both
+  // run without branches: past the span the second step sees tiles flagged
+  // invalid (zeros, fully masked), and the last stage converts its own tile
+  // once more into the image nobody reads again.
   if (nstages > 0) {
-    fetch(0);
-    convert(stage[0]);
-    if (nstages > 1) fetch(1);
+    fetch_k(0);
+    fetch_v(0);
+    convert(0, true);
+    convert(0, false);
+    if (nstages > 1) {
+      fetch_k(1);
+      fetch_v(1);
+    }
   }
   lds_barrier();
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
     const uint16_t *img = stage[buf];
-    step(img, s, 0, buf);
-    if (s * kStageTiles + 2 < ntiles) step(img, s, 1, buf);
-    if (s + 1 < nstages) {
-      convert(stage[buf ^ 1]);
-      if (s + 2 < nstages) fetch(s + 2);
-    }
+    // the stage's tile flags, one LDS read (uniform bit mask)
+    const u4 okw = *(const u4 *)s_valid[buf];
+    const int okv = __builtin_amdgcn_readfirstlane((okw.x != 0) | ((okw.y != 0) << 1) | ((okw.z != 0) << 2) |
+                                                   ((okw.w != 0) << 3));
+    f4 S0[2][RB], S1[2][RB];
+    float mb0[RB], mb1[RB], v[RB][8];
+    OT P[RB];
+    qk(img, 0, S0, mb0);
+    scores(S0, mb0, s, 0, okv, v);
+    qk(img, 1, S1, mb1);
+    probs(v, P);
+    pv(img, 0, P);
+    convert(buf ^ 1, true);
+    if (s + 2 < nstages) fetch_k(s + 2);
+    scores(S1, mb1, s, 1, okv, v);
+    probs(v, P);
+    pv(img, 1, P);
+    convert(buf ^ 1, false);
+    if (s + 2 < nstages) fetch_v(s + 2);
     lds_barrier();
   }
 
