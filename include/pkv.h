@@ -87,15 +87,18 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
                         const int32_t *start_pos, const int32_t *widths, int32_t *new_lens);
 
 /*
- * Causal GQA paged attention for decode (num_queries = 1) and speculative
- * verify (num_queries = 1 + drafts), dequantization fused into the page load.
- * Replaces paged_attention and its Metal kernel
- * (src/mlx_one/engine/paged_attention.py:62-124 kernel, :127-206 dispatch and
- * partition merge).  The reference splits each sequence into fixed token
- * partitions; here the 16-token tiles of all (sequence, KV head) pairs are
- * shared out as equal runs over `waves` waves, and a pair whose tiles span
- * several runs is merged by log-sum-exp (:191-204) in a second kernel on the
- * same stream.
+ * Causal GQA paged attention for decode (num_queries = 1), speculative
+ * verify (num_queries = 1 + drafts) and chunked prefill (wide query blocks),
+ * dequantization fused into the page load.  Replaces paged_attention and its
+ * Metal kernel (src/mlx_one/engine/paged_attention.py:62-124 kernel, :127-206
+ * dispatch and partition merge).  Up to 32 query rows per KV head
+ * (num_queries x num_heads / num_kv_heads; 16 at head_dim > 128): the
+ * reference splits each sequence into fixed token partitions; here the
+ * 16-token tiles of all (sequence, KV head) pairs are shared out as equal runs
+ * over `waves` waves, and a pair whose tiles span several runs is merged by
+ * log-sum-exp (:191-204) in a second kernel on the same stream.  Wider query
+ * blocks (up to 2^24 rows per KV head) run on an MFMA prefill kernel, 128
+ * rows per workgroup, that needs no workspace and ignores `waves`.
  *
  *  queries      : [batch][num_heads][num_queries][head_dim], float_kind
  *  seq_lens     : [batch] tokens in each sequence's cache (after the append)
@@ -117,10 +120,12 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
                         int64_t workspace_bytes, void *out);
 
 /* Waves the attention kernel keeps resident on the current device for this
- * layout and (num_heads, num_queries): the default `waves`.  <0 on error. */
+ * layout and (num_heads, num_queries): the default `waves` (1 for query
+ * blocks served by the prefill kernel).  <0 on error. */
 int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries);
 
-/* Workspace bytes pkv_paged_attention needs for `waves` work waves. */
+/* Workspace bytes pkv_paged_attention needs for `waves` work waves (0 for
+ * query blocks served by the prefill kernel). */
 int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
                                       int32_t num_queries, int32_t waves);
 

@@ -146,8 +146,9 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     """Attention of ``queries [B, H, Q, D]`` over the paged cache.
 
     ``seq_lens`` counts the tokens in each sequence's cache (after the
-    append) and stays on the device: the kernel shares the tiles of all
-    sequences out over ``waves`` waves (default: the resident capacity).
+    append) and stays on the device: the decode kernel shares the tiles of
+    all sequences out over ``waves`` waves (default: the resident capacity);
+    query blocks past 32 rows per KV head run on the prefill kernel.
     ``workspace`` (bytes from ``workspace_bytes``) may be given by the caller.
     """
     if queries.dim() != 4:
