@@ -167,6 +167,12 @@ def cpu_baseline(w, inst, layer, device, budget_s):
         sub = slice(0, rows)
         if w.bits != 16 and w.append_tokens:
             cport.quantize_rows(new[:rows * w.kv_heads * 2 * w.append_tokens], w.bits, w.group_size)
+        if w.bits == 16:                      # float pages: (K, V) bits in the page dtype
+            return cport.paged_attention(q[sub], inst.table[sub], lengths[sub], positions[sub],
+                                         widths[sub], heads_kv=w.kv_heads,
+                                         page_tokens=w.page_tokens, bits=0, float_pages=host,
+                                         float_f16=fmt.dtype == torch.float16, scale=scale,
+                                         threads=cores)
         return cport.paged_attention(q[sub], inst.table[sub], lengths[sub], positions[sub],
                                      widths[sub], heads_kv=w.kv_heads, page_tokens=w.page_tokens,
                                      bits=w.bits, group_size=w.group_size, pages=host,

@@ -134,17 +134,23 @@ __device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int h
 }
 
 // Log-sum-exp merge of partition partials (paged_attention.py:191-204, in
-// the exp2 domain): one wave per (segment, query row) of a segment split over
-// several waves' runs; whole segments were written by the attention kernel.
-// Lane k holds piece k's weight 2^(m_k - M) / S; the output row accumulates
-// over the pieces with the lanes striding its DP columns.
+// the exp2 domain): one 4-wave workgroup per (segment, query row) of a segment
+// split over several waves' runs; whole segments were written by the
+// attention kernel.  Every wave finds M = max m and S = sum l 2^(m - M) over
+// the pieces (lanes stride the pieces); then wave w takes pieces w, w+4, ...,
+// with up to 16 partial rows in flight at once (lanes stride the DP columns),
+// and the four sums meet in LDS.  The merge is thus two memory round trips
+// whatever the number of pieces up to 64.
 template <int DP>
 __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
   constexpr int PER = DP / 64 > 0 ? DP / 64 : 1;  // output columns per lane
+  constexpr int NW = 4;                           // waves per workgroup
+  constexpr int KW = 16;                          // pieces per wave in flight
+  __shared__ float s_acc[NW - 1][64 * PER];
   const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (gw >= a.batch * a.hk * a.rows) return;
-  const int row = gw % a.rows, seg = gw / a.rows;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = blockIdx.x;
+  const int row = unit % a.rows, seg = unit / a.rows;
   const int b = seg / a.hk, kh = seg % a.hk;
   // tiles before sequence b, and the launch's split (as the attention kernel made it)
   int pre = 0, tiles = 0;
@@ -160,16 +166,14 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
   Split sp;
   sp.init(T, min(a.waves, T));
   const SegPieces pc = seg_pieces(sp, s0, s0 + ntb);
-  if (pc.n < 2) return;
+  if (pc.n < 2) return;  // the same for every wave of the workgroup
 
   // M = max m, S = sum l 2^(m - M) over the pieces (lanes stride the pieces)
   float mx = -INFINITY, sm = 0.0f;
-  float2 mine = make_float2(-INFINITY, 0.0f);  // lane k's piece (k < 64), reused for its weight
   for (int k0 = 0; k0 < pc.n; k0 += 64) {
     const int k = k0 + lane;
     if (k < pc.n) {
       const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
-      if (k0 == 0) mine = ml;
       if (ml.y > 0.0f) {  // a piece with no visible token holds l = 0
         const float nm = fmaxf(mx, ml.x);
         sm = sm * __builtin_amdgcn_exp2f(mx - nm) + ml.y * __builtin_amdgcn_exp2f(ml.x - nm);
@@ -189,41 +193,56 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
   float acc[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) acc[i] = 0.0f;
-  for (int k0 = 0; k0 < pc.n; k0 += 64) {
-    // lane j: weight of piece k0 + j
+  for (int k0 = 0; k0 < pc.n; k0 += NW * KW) {
+    // this wave's pieces k0 + wv + 4i: their partial rows, all requested at once
+    float x[KW][PER];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+      const int k = k0 + wv + NW * i;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[i][e] = 0.0f;
+      if (k < pc.n) {
+        const float *src = a.part_acc + ((int64_t)pc.slot(k) * a.rows + row) * DP + lane * PER;
+        if constexpr (PER == 4) {
+          const f4 v = *(const f4 *)src;
+          x[i][0] = v[0]; x[i][1] = v[1]; x[i][2] = v[2]; x[i][3] = v[3];
+        } else if constexpr (PER == 2) {
+          const float2 v = *(const float2 *)src;
+          x[i][0] = v.x; x[i][1] = v.y;
+        } else {
+          x[i][0] = src[0];
+        }
+      }
+    }
+    // lane l: weight 2^(m - M) / S of piece k0 + l
     float wl = 0.0f;
     {
       const int k = k0 + lane;
       if (k < pc.n) {
-        const float2 ml =
-            k0 == 0 ? mine : *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
+        const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
         wl = ml.y > 0.0f ? __builtin_amdgcn_exp2f(ml.x - mx) * inv : 0.0f;
       }
     }
-    const int kn = min(64, pc.n - k0);
-#pragma unroll 8
-    for (int j = 0; j < kn; ++j) {
-      const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
-      const float *src = a.part_acc + ((int64_t)pc.slot(k0 + j) * a.rows + row) * DP + lane * PER;
-      if constexpr (PER == 4) {
-        const f4 x = *(const f4 *)src;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += wk * x[i];
-      } else if constexpr (PER == 2) {
-        const float2 x = *(const float2 *)src;
-        acc[0] += wk * x.x;
-        acc[1] += wk * x.y;
-      } else {
-        acc[0] += wk * src[0];
-      }
+    for (int i = 0; i < KW; ++i) {
+      const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), wv + NW * i));
+#pragma unroll
+      for (int e = 0; e < PER; ++e) acc[e] += wk * x[i][e];
     }
   }
+  if (wv > 0) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) s_acc[wv - 1][lane * PER + e] = acc[e];
+  }
+  __syncthreads();
+  if (wv != 0) return;
   const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
   uint16_t *o = a.out + (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane * PER + i;
-    if (d < a.dim) o[d] = float_to_bits(acc[i], a.float_kind);
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane * PER + e;
+    const float v = acc[e] + s_acc[0][d] + s_acc[1][d] + s_acc[2][d];
+    if (d < a.dim) o[d] = float_to_bits(v, a.float_kind);
   }
 }
 
@@ -812,9 +831,10 @@ hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
 }
 
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a) {
-  const int64_t waves = (int64_t)a.batch * a.hk * a.rows;
-  if (waves == 0 || a.waves <= 1) return hipSuccess;  // one run covers every segment whole
-  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  const int64_t units = (int64_t)a.batch * a.hk * a.rows;  // one workgroup per (segment, row)
+  if (units == 0 || a.waves <= 1) return hipSuccess;  // one run covers every segment whole
+  if (units > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)units), block(256);
   if (a.dp == 64) hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, stream, a);
   else if (a.dp == 128) hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, stream, a);
   else if (a.dp == 256) hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, stream, a);
