@@ -8,15 +8,16 @@
 // 512 queries x 4 heads = 2048 rows per KV head), where the contraction is
 // dense and MFMA-bound.
 //
-// Work unit = one workgroup of 4 waves = (sequence, KV head, block of 4*16*RB
+// Work unit = one workgroup of 8 waves = (sequence, KV head, block of 8*16*RB
 // query rows); wave w owns 16*RB rows as RB 16-column MFMA row tiles.  The
-// span is streamed in stages of 4 tiles (64 tokens).  Per stage each wave
+// span is streamed in stages of 8 tiles (128 tokens).  Per stage each wave
 // loads ONE tile of quantized K/V (plus its scale/bias words) from HBM into
 // registers a stage ahead, dequantizes it once (packed f16: (1024+c) - 1024,
 // then c*scale + bias) and writes the f16 image into the LDS stage buffer
-// that all four waves read: K as [tile][token][dim], V transposed as
-// [dim][token slot].  Dequantization thus costs 1/4 tile per wave, and the
-// inner loop is a plain f16 flash-attention step:
+// that all eight waves read: K as [tile][token][dim], V transposed as
+// [dim][token slot].  Dequantization thus costs 1/8 of the span per wave, a
+// stage's four steps give the next stage's loads time to land, and the inner
+// loop is a plain f16 flash-attention step:
 //   S^T = K.Q^T        v_mfma_f32_16x16x32_f16, two tiles per step
 //   online softmax     per column, exp2 domain, lazy rescale
 //   O^T += V^T.P^T     v_mfma_f32_16x16x32_f16 over the step's 32 tokens
@@ -32,24 +33,28 @@
 
 namespace pkv {
 
-constexpr int kPrefillWaves = 4;
-constexpr int kStageTiles = kPrefillWaves;  // each wave converts one tile per stage
+// Waves per workgroup, = tiles per stage (each wave converts one tile per
+// stage): 8, or 4 at head_dim 256 (LDS budget of the double-buffered image).
+constexpr int prefill_waves(int dp) { return dp > 128 ? 4 : 8; }
+constexpr int kMaxPrefillWaves = 8;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Row blocks per wave: two 16-column blocks up to head_dim 128, one beyond
 // (register budget of the O accumulators).
 constexpr int prefill_rb(int dp) { return dp > 128 ? 1 : 2; }
-constexpr int prefill_rows(int dp) { return kPrefillWaves * 16 * prefill_rb(dp); }
+constexpr int prefill_rows(int dp) { return prefill_waves(dp) * 16 * prefill_rb(dp); }
 
 // LDS image of one stage (u16 elements).  Rows padded by 8 elements so that
-// the 16 lanes of a ds_read_b128 phase hit distinct banks.
+// the 16 lanes of a ds_read_b128 phase hit distinct banks (row strides of
+// 2*(DP+8) and 272 bytes).
 template <int DP>
 struct StageImage {
-  static constexpr int KROW = DP + 8;                // K row: one token
+  static constexpr int TILES = prefill_waves(DP);
+  static constexpr int KROW = DP + 8;           // K row: one token
   static constexpr int KTILE = 16 * KROW;
-  static constexpr int VROW = 16 * kStageTiles + 8;  // V^T row: one dim, 64 token slots
-  static constexpr int K_ELEMS = kStageTiles * KTILE;
+  static constexpr int VROW = 16 * TILES + 8;   // V^T row: one dim, 16 token slots per tile
+  static constexpr int K_ELEMS = TILES * KTILE;
   static constexpr int ELEMS = K_ELEMS + DP * VROW;
 };
 
@@ -62,7 +67,9 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int BITS, int DP, int G, int FK>
-__global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const AttnArgs a) {
+  constexpr int kPrefillWaves = prefill_waves(DP);
+  constexpr int kStageTiles = kPrefillWaves;
   constexpr int RB = prefill_rb(DP);
   constexpr int ROWS = prefill_rows(DP);
   using C = Cfg<BITS, DP, G, RB, FK, 1>;
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
     tip = 0;
     if (t < ntiles) {
       const int p = t >> tpp_shift;
-      if (p >= wbase + 64) {  // pages advance at most 4 per stage
+      if (p >= wbase + 64) {  // pages advance at most 8 per stage
         pwin = pnext;
         wbase += 64;
         pnext = load_ids(wbase + 64);
@@ -449,25 +456,36 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnArgs a) {
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
     const uint16_t *img = stage[buf];
-    // the stage's tile flags, one LDS read (uniform bit mask)
-    const u4 okw = *(const u4 *)s_valid[buf];
-    const int okv = __builtin_amdgcn_readfirstlane((okw.x != 0) | ((okw.y != 0) << 1) | ((okw.z != 0) << 2) |
-                                                   ((okw.w != 0) << 3));
-    f4 S0[2][RB], S1[2][RB];
-    float mb0[RB], mb1[RB], v[RB][8];
+    // the stage's tile flags (uniform bit mask)
+    int okv = 0;
+#pragma unroll
+    for (int q4 = 0; q4 < kStageTiles / 4; ++q4) {
+      const u4 okw = *(const u4 *)&s_valid[buf][4 * q4];
+      okv |= ((okw.x != 0) | ((okw.y != 0) << 1) | ((okw.z != 0) << 2) | ((okw.w != 0) << 3)) << (4 * q4);
+    }
+    okv = __builtin_amdgcn_readfirstlane(okv);
+    // steps over tile pairs; pair pr+1's QK MFMAs are issued before pair
+    // pr's exponentials, the conversion halves sit beside the first two
+    // pairs' PV MFMAs
+    constexpr int NPAIR = kStageTiles / 2;
+    f4 S[2][2][RB];
+    float mb[2][RB], v[RB][8];
     OT P[RB];
-    qk(img, 0, S0, mb0);
-    scores(S0, mb0, s, 0, okv, v);
-    qk(img, 1, S1, mb1);
-    probs(v, P);
-    pv(img, 0, P);
-    convert(buf ^ 1, true);
-    if (s + 2 < nstages) fetch_k(s + 2);
-    scores(S1, mb1, s, 1, okv, v);
-    probs(v, P);
-    pv(img, 1, P);
-    convert(buf ^ 1, false);
-    if (s + 2 < nstages) fetch_v(s + 2);
+    qk(img, 0, S[0], mb[0]);
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) {
+      scores(S[pr & 1], mb[pr & 1], s, pr, okv, v);
+      if (pr + 1 < NPAIR) qk(img, pr + 1, S[(pr + 1) & 1], mb[(pr + 1) & 1]);
+      probs(v, P);
+      pv(img, pr, P);
+      if (pr == 0) {
+        convert(buf ^ 1, true);
+        if (s + 2 < nstages) fetch_k(s + 2);
+      } else if (pr == 1) {
+        convert(buf ^ 1, false);
+        if (s + 2 < nstages) fetch_v(s + 2);
+      }
+    }
     lds_barrier();
   }
 
@@ -531,7 +549,7 @@ hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a) {
   const int64_t blocks = (int64_t)a.batch * a.g.hk * ((a.rows + rows_per_block - 1) / rows_per_block);
   if (blocks == 0) return hipSuccess;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(64 * kPrefillWaves), 0, stream, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(64 * prefill_waves(a.g.dp)), 0, stream, a);
   return hipGetLastError();
 }
 
