@@ -1,0 +1,227 @@
+"""Paged branch of the reference's ``CacheManager`` (``engine/cache_manager.py``).
+
+Same names and error behaviour for the calls the paged path makes:
+``create_handle`` (one ``PagedKVCache`` per layer, key/value types ``f16`` /
+``bf16`` / ``q8_0`` / ``q4_0`` -> bits None/None/8/4, :152-200),
+``estimate_growth`` (the quantized growth formula of :255-262, with this
+build's group size in place of 32), ``reserve`` / ``commit`` / ``reconcile`` /
+``release_reservation`` / ``transient_reservation`` (a byte budget; over budget
+raises ``CacheCapacityError``), ``release``, ``stats``, ``close``.  The arena
+(``block_pool``) is a ``SegmentedPageArena`` whose pages live in device pools.
+Dense / block / hybrid backends, prefix indexing, quality qualification and
+host admission are outside the paged path and raise on use.
+"""
+
+from __future__ import annotations
+
+import threading
+import uuid
+from contextlib import contextmanager
+from dataclasses import dataclass, field
+
+from pkv.arena import SegmentedPageArena
+from pkv.cache_errors import CacheCapacityError, CacheCorruptionError, KVQuantizationUnsupported
+from pkv.paged import PagedKVCache
+
+_BITS = {"f16": None, "bf16": None, "q8_0": 8, "q4_0": 4}
+
+
+@dataclass(frozen=True)
+class CacheConfig:
+    backend: str = "paged"
+    block_size_tokens: int = 16
+    key_type: str = "bf16"
+    value_type: str = "bf16"
+    memory_budget_bytes: int = 8 << 30
+    group_size: int = 32
+    prefix_cache_enabled: bool = False
+
+
+@dataclass
+class CacheBundle:
+    entries: tuple
+    closed: bool = False
+
+    @property
+    def nbytes(self):
+        return sum(e.nbytes for e in self.entries)
+
+    @property
+    def offset(self):
+        return max((e.offset for e in self.entries), default=0)
+
+
+@dataclass
+class CacheReservation:
+    reservation_id: str
+    nbytes: int
+    handle_id: str | None = None
+    committed: bool = False
+    released: bool = False
+
+
+@dataclass
+class CacheHandle:
+    handle_id: str
+    request_id: str
+    sequence_id: str
+    bundle: CacheBundle
+    backend: str
+    key_type: str
+    token_count: int = 0
+    reserved_bytes: int = 0
+    closed: bool = False
+    reservation: CacheReservation | None = None
+    metadata: dict = field(default_factory=dict)
+
+
+@dataclass(frozen=True)
+class CacheMemoryStats:
+    budget_bytes: int
+    reserved_bytes: int
+    transient_bytes: int
+    allocated_bytes: int
+    live_handles: int
+    arena: dict
+
+
+class CacheManager:
+    def __init__(self, bundle, config: CacheConfig = CacheConfig(), *, device="cuda"):
+        if config.backend != "paged":
+            raise ValueError("this build serves the paged backend only")
+        self.bundle, self.config = bundle, config
+        self.block_pool = SegmentedPageArena(config.memory_budget_bytes,
+                                             block_tokens=config.block_size_tokens, device=device)
+        self._lock = threading.RLock()
+        self._handles = {}
+        self._reserved = 0
+        self._transient = 0
+        self._closed = False
+
+    @property
+    def layer_specs(self):
+        return self.bundle.spec.layers
+
+    def _ensure_open(self):
+        if self._closed:
+            raise CacheCorruptionError("cache manager is closed")
+
+    # -- handles -------------------------------------------------------------------
+    def create_handle(self, request_id, *, sequence_id=None, key_type="f16", value_type="f16"):
+        with self._lock:
+            self._ensure_open()
+            if key_type != value_type or key_type not in _BITS:
+                raise KVQuantizationUnsupported("paged KV requires matched precision")
+            bits = _BITS[key_type]
+            dtype = "bfloat16" if key_type == "bf16" else "float16"
+            entries = tuple(PagedKVCache(self.block_pool, layer_id=s.layer_id, dtype=dtype,
+                                         bits=bits, group_size=self.config.group_size)
+                            for s in self.layer_specs)
+            handle = CacheHandle(f"cache-{uuid.uuid4().hex}", request_id,
+                                 sequence_id or request_id, CacheBundle(entries), "paged",
+                                 key_type)
+            self._handles[handle.handle_id] = handle
+            return handle
+
+    def _validate_handle(self, handle):
+        if handle.closed or self._handles.get(handle.handle_id) is not handle:
+            raise CacheCorruptionError("unknown or closed cache handle")
+
+    def estimate_growth(self, handle, prompt_tokens, max_new_tokens=0):
+        """Bytes the handle may grow by (``cache_manager.py:217-266``)."""
+        self._validate_handle(handle)
+        tokens = max(int(prompt_tokens) + int(max_new_tokens) - handle.bundle.offset, 0)
+        bits = _BITS[handle.key_type]
+        if bits is None:
+            amount = self.bundle.spec.bytes_per_token() * tokens
+        else:
+            g = self.config.group_size
+            amount = sum(s.num_kv_heads * tokens * sum(
+                ((dim + g - 1) // g) * (g * bits // 8 + 4) for dim in (s.key_head_dim, s.value_head_dim))
+                for s in self.layer_specs)
+            # page-granular sealing overlap (the reference's tail allowance)
+            amount += self.bundle.spec.bytes_per_token() * self.config.block_size_tokens * 16
+        handle.metadata["admission_request"] = {"prompt_tokens": prompt_tokens,
+                                                "requested_output_tokens": max_new_tokens,
+                                                "total_growth_bytes": amount}
+        return amount
+
+    # -- byte budget -------------------------------------------------------------------
+    def reserve(self, handle, nbytes):
+        with self._lock:
+            self._ensure_open()
+            self._validate_handle(handle)
+            nbytes = int(nbytes)
+            if nbytes < 0:
+                raise ValueError("negative reservation")
+            if self._reserved + self._transient + nbytes > self.config.memory_budget_bytes:
+                raise CacheCapacityError("paged cache budget exhausted", retryable=True)
+            self._reserved += nbytes
+            reservation = CacheReservation(f"resv-{uuid.uuid4().hex}", nbytes, handle.handle_id)
+            handle.reservation = reservation
+            handle.reserved_bytes += nbytes
+            return reservation
+
+    def commit(self, reservation, allocated_bytes=0):
+        with self._lock:
+            if reservation.released:
+                raise CacheCorruptionError("reservation already released")
+            reservation.committed = True
+
+    def release_reservation(self, reservation):
+        with self._lock:
+            if reservation.released:
+                return
+            reservation.released = True
+            self._reserved -= reservation.nbytes
+            handle = self._handles.get(reservation.handle_id)
+            if handle is not None:
+                handle.reserved_bytes -= reservation.nbytes
+                if handle.reservation is reservation:
+                    handle.reservation = None
+
+    def reconcile(self, handle):
+        """Refresh the handle's token count from its caches."""
+        with self._lock:
+            self._validate_handle(handle)
+            handle.token_count = handle.bundle.offset
+
+    @contextmanager
+    def transient_reservation(self, nbytes):
+        with self._lock:
+            self._ensure_open()
+            nbytes = int(nbytes)
+            if self._reserved + self._transient + nbytes > self.config.memory_budget_bytes:
+                raise CacheCapacityError("transient reservation exceeds the cache budget",
+                                         retryable=True)
+            self._transient += nbytes
+        try:
+            yield nbytes
+        finally:
+            with self._lock:
+                self._transient -= nbytes
+
+    def release(self, handle):
+        with self._lock:
+            if handle.closed:
+                raise CacheCorruptionError("cache handle released twice")
+            self._validate_handle(handle)
+            for entry in handle.bundle.entries:
+                entry.reset()
+            if handle.reservation is not None:
+                self.release_reservation(handle.reservation)
+            handle.bundle.closed = handle.closed = True
+            del self._handles[handle.handle_id]
+
+    def stats(self):
+        with self._lock:
+            return CacheMemoryStats(self.config.memory_budget_bytes, self._reserved,
+                                    self._transient, self.block_pool.allocated_nbytes,
+                                    len(self._handles), self.block_pool.stats())
+
+    def close(self):
+        with self._lock:
+            for handle in list(self._handles.values()):
+                self.release(handle)
+            self.block_pool.clear()
+            self._closed = True

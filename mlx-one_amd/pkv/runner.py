@@ -1,0 +1,158 @@
+"""``PagedRunner.execute``: a batch step over paged caches (``engine/paged.py:285-417``).
+
+Same flow and checks as the reference, with this build's attention stack as
+the model: validate the batch (same model, phase, layer count; every cache a
+``PagedKVCache`` of its layer in the model's activation dtype; one pool and
+precision), reserve the step's transient bytes on the cache manager, **clone**
+every layer cache (sealed pages shared, mutable tails copied: the drafts),
+run the layers over ``PagedBatchCache`` views of the drafts (append +
+attention per layer), pick each request's outputs (all positions for
+``return_all_logits``, else the last), then **commit** the drafts into the
+request caches and release the rest.  A failure anywhere leaves the request
+caches untouched.  Requests carry hidden states ``[T, hidden]`` where the
+reference carries token ids: embedding and LM head sit outside the path.
+"""
+
+from __future__ import annotations
+
+import time
+from contextlib import ExitStack
+from dataclasses import dataclass
+
+from pkv.modes import ModelCapabilityUnsupported
+from pkv.paged import KERNEL_VERSION, PagedBatchCache, PagedKVCache
+
+
+@dataclass(frozen=True)
+class ForwardRequest:
+    """Subset of ``engine/batching.py:50-66`` the paged runner reads."""
+
+    request_id: str
+    hidden: object                 # [T, hidden] device tensor, activation dtype
+    cache: tuple                   # one PagedKVCache per layer
+    phase: str = "decode"
+    runtime: object = None         # CacheManager
+    handle: object = None          # CacheHandle owning ``cache``
+    model_epoch: int = 0
+    return_all_logits: bool = False
+
+    @property
+    def token_ids(self):
+        return range(int(self.hidden.shape[0]))
+
+
+@dataclass(frozen=True)
+class RunnerOutput:
+    """``engine/contracts.py:196-210``: per request, its outputs and committed tokens."""
+
+    request_ids: tuple
+    logits: tuple                  # per request [1, n or 1, hidden]
+    committed_token_counts: tuple
+
+    def __post_init__(self):
+        if len(set(self.request_ids)) != len(self.request_ids):
+            raise ValueError("runner output request IDs must be unique")
+        if len(self.request_ids) != len(self.committed_token_counts):
+            raise ValueError("runner output mappings must align")
+        if any(count < 0 for count in self.committed_token_counts):
+            raise ValueError("committed counts cannot be negative")
+        if len(self.logits) != len(self.request_ids):
+            raise ValueError("runner logits must align with request IDs")
+
+
+class PagedRunner:
+    def __init__(self, model):
+        self.model = model
+        self.last_trace = {}
+
+    def _validate(self, requests):
+        if not requests:
+            raise ValueError("empty paged batch")
+        first = requests[0]
+        layers = self.model.spec.layers
+        for r in requests:
+            if r.phase != first.phase or r.model_epoch != first.model_epoch \
+                    or len(r.cache) != len(first.cache):
+                raise ValueError("incompatible paged batch")
+            if (not r.cache or any(not isinstance(c, PagedKVCache) for c in r.cache)
+                    or len({c.offset for c in r.cache}) != 1
+                    or any(c.layer_id != i for i, c in enumerate(r.cache))
+                    or len(r.cache) != len(layers)):
+                raise ValueError("invalid paged layer mappings")
+            if r.handle is not None:
+                r.runtime._validate_handle(r.handle)
+                if r.handle.bundle.entries is not r.cache:
+                    raise ValueError("paged request does not own its cache mapping")
+            if int(r.hidden.shape[0]) < 1 or int(r.hidden.shape[-1]) != self.model.spec.hidden:
+                raise ValueError("request hidden states do not match the model")
+            for cache, layout in zip(r.cache, layers, strict=True):
+                if cache.dtype != self.model.activation_dtype:
+                    raise ModelCapabilityUnsupported("paged storage differs from execution precision")
+                for reference in cache._blocks:
+                    stored = reference.block.layout
+                    if (stored.num_kv_heads != layout.kv_heads or stored.head_dim != layout.key_dim
+                            or stored.layer_id != layout.layer_id):
+                        raise ValueError("paged layer layout differs from the model")
+        if len({(id(c.pool), c.dtype, c.bits) for r in requests for c in r.cache}) != 1:
+            raise ValueError("incompatible paged pools or precision")
+        if any(r.runtime is not first.runtime for r in requests):
+            raise ValueError("paged batch spans cache managers")
+
+    def execute(self, requests):
+        import torch
+
+        requests = tuple(requests)
+        self._validate(requests)
+        first = requests[0]
+        spec = self.model.spec
+        widths = tuple(int(r.hidden.shape[0]) for r in requests)
+        width = max(widths)
+        started = time.perf_counter()
+        metrics = {"direct_attention_calls": 0, "kernel_version": KERNEL_VERSION,
+                   "synchronized_kernel_dispatch_ms": 0.0}
+        # transient bytes of the step: activations and projections per layer
+        transient = len(requests) * width * spec.num_layers * 4 * (
+            spec.hidden + (spec.query_heads + 2 * spec.kv_heads) * spec.head_dim) * 2
+        runtime = first.runtime
+        drafts = []
+        outputs = []
+        with ExitStack() as stack:
+            if runtime is not None:
+                stack.enter_context(runtime.transient_reservation(transient))
+            try:
+                for r in requests:
+                    drafts.append([c.clone() for c in r.cache])
+                packed = tuple(PagedBatchCache(tuple(d[layer] for d in drafts), widths, metrics)
+                               for layer in range(len(first.cache)))
+                device = first.hidden.device
+                x = torch.zeros((len(requests), width, spec.hidden), dtype=first.hidden.dtype,
+                                device=device)
+                positions = torch.zeros((len(requests), width), dtype=torch.int64)
+                for i, r in enumerate(requests):
+                    x[i, :widths[i]] = r.hidden
+                    start = r.cache[0].offset
+                    positions[i, :widths[i]] = torch.arange(start, start + widths[i])
+                y = self.model.forward(x, cache=packed, position_ids=positions.to(device))
+                for i, n in enumerate(widths):
+                    begin = 0 if requests[i].return_all_logits else n - 1
+                    outputs.append(y[i:i + 1, begin:n].clone())
+                # commit: the drafts become the request caches (old refs closed)
+                for r, layers in zip(requests, drafts, strict=True):
+                    for cache, draft in zip(r.cache, layers, strict=True):
+                        cache.replace_from(draft)
+                    if r.handle is not None:
+                        r.handle.token_count = r.cache[0].offset
+            finally:
+                for layers in drafts:
+                    for draft in layers:
+                        draft.reset()   # no-op for committed drafts (emptied by replace_from)
+        self.last_trace = {**metrics, "phase": first.phase,
+                           "request_ids": [r.request_id for r in requests],
+                           "batch_size": len(requests),
+                           "history_lengths": [r.cache[0].offset - w for r, w in zip(requests, widths)],
+                           "real_tokens": sum(widths), "padded_tokens": len(requests) * width,
+                           "padding_efficiency": sum(widths) / (len(requests) * width),
+                           "transient_reserved_bytes": transient,
+                           "layer_layouts": [vars(layer) for layer in spec.layers],
+                           "duration_ms": (time.perf_counter() - started) * 1000}
+        return RunnerOutput(tuple(r.request_id for r in requests), tuple(outputs), widths)

@@ -1,0 +1,121 @@
+"""Host logic of the paged ``CacheManager`` and ``PagedRunner`` validation (no GPU).
+
+Restates the reference's paged branches (``engine/cache_manager.py:152-200``
+create_handle precision rules, :255-262 quantized growth formula) and the
+runner's batch checks (``engine/paged.py:308-335``).
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from pkv.cache_errors import CacheCapacityError, CacheCorruptionError, KVQuantizationUnsupported
+from pkv.cache_manager import CacheConfig, CacheManager
+from pkv.layer import ModelSpec
+from pkv.paged import PagedKVCache
+from pkv.runner import ForwardRequest, PagedRunner, RunnerOutput
+
+
+class _Bundle:
+    def __init__(self, spec):
+        self.spec = spec
+        self.activation_dtype = spec.dtype
+
+
+def _manager(**kw):
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=3,
+                     dtype=kw.pop("dtype", "bfloat16"))
+    return CacheManager(_Bundle(spec), CacheConfig(**kw), device="cpu")
+
+
+def test_create_handle_precision_rules():
+    cm = _manager()
+    h = cm.create_handle("r1", key_type="q8_0", value_type="q8_0")
+    assert len(h.bundle.entries) == 3
+    assert all(isinstance(e, PagedKVCache) for e in h.bundle.entries)
+    assert [e.layer_id for e in h.bundle.entries] == [0, 1, 2]
+    assert {e.bits for e in h.bundle.entries} == {8} and {e.dtype for e in h.bundle.entries} == {"float16"}
+    h4 = cm.create_handle("r2", key_type="q4_0", value_type="q4_0")
+    assert {e.bits for e in h4.bundle.entries} == {4}
+    hb = cm.create_handle("r3", key_type="bf16", value_type="bf16")
+    assert {e.dtype for e in hb.bundle.entries} == {"bfloat16"} and {e.bits for e in hb.bundle.entries} == {None}
+    with pytest.raises(KVQuantizationUnsupported):
+        cm.create_handle("r4", key_type="q8_0", value_type="f16")
+    with pytest.raises(KVQuantizationUnsupported):
+        cm.create_handle("r5", key_type="q2_k", value_type="q2_k")
+    assert cm.stats().live_handles == 3
+
+
+def test_estimate_growth_matches_the_reference_formula():
+    cm = _manager(block_size_tokens=16, group_size=32)
+    h = cm.create_handle("r", key_type="q8_0", value_type="q8_0")
+    # HK * tokens * sum over (Dk, Dv) ceil(D/32) * (32*bits/8 + 4), per layer,
+    # plus bytes_per_token * block * 16 (cache_manager.py:255-262)
+    per_layer = 2 * 100 * 2 * ((64 + 31) // 32) * (32 * 8 // 8 + 4)
+    allowance = 3 * 2 * 2 * 64 * 2 * 16 * 16
+    assert cm.estimate_growth(h, 60, 40) == 3 * per_layer + allowance
+    hf = cm.create_handle("f", key_type="f16", value_type="f16")
+    assert cm.estimate_growth(hf, 10) == 3 * 2 * 2 * 64 * 2 * 10
+
+
+def test_budget_reservations_and_release():
+    cm = _manager(memory_budget_bytes=1000)
+    h = cm.create_handle("r", key_type="bf16", value_type="bf16")
+    r = cm.reserve(h, 600)
+    with pytest.raises(CacheCapacityError):
+        cm.reserve(h, 500)
+    with pytest.raises(CacheCapacityError):
+        with cm.transient_reservation(500):
+            pass
+    cm.release_reservation(r)
+    with cm.transient_reservation(900) as n:
+        assert n == 900 and cm.stats().transient_bytes == 900
+    assert cm.stats().transient_bytes == 0
+    cm.release(h)
+    with pytest.raises(CacheCorruptionError):
+        cm.release(h)
+    with pytest.raises(CacheCorruptionError):
+        cm.estimate_growth(h, 1)
+    cm.close()
+    with pytest.raises(CacheCorruptionError):
+        cm.create_handle("late", key_type="bf16", value_type="bf16")
+
+
+class _Hidden:
+    def __init__(self, tokens, hidden):
+        self.shape = (tokens, hidden)
+
+
+class _Model:
+    def __init__(self, spec):
+        self.spec, self.activation_dtype = spec, spec.dtype
+
+
+def test_runner_rejects_inconsistent_batches():
+    cm = _manager()
+    runner = PagedRunner(_Model(cm.bundle.spec))
+    h1 = cm.create_handle("a", key_type="bf16", value_type="bf16")
+    h2 = cm.create_handle("b", key_type="bf16", value_type="bf16")
+    ok = ForwardRequest("a", _Hidden(1, 256), h1.bundle.entries, runtime=cm, handle=h1)
+    with pytest.raises(ValueError):
+        runner.execute([])
+    with pytest.raises(ValueError):        # another phase in the batch
+        runner._validate([ok, ForwardRequest("b", _Hidden(1, 256), h2.bundle.entries,
+                                             phase="prefill", runtime=cm, handle=h2)])
+    with pytest.raises(ValueError):        # layers out of order
+        runner._validate([ForwardRequest("a", _Hidden(1, 256), h1.bundle.entries[::-1],
+                                         runtime=cm)])
+    with pytest.raises(ValueError):        # the request does not own its caches
+        runner._validate([ForwardRequest("a", _Hidden(1, 256), h2.bundle.entries, runtime=cm,
+                                         handle=h1)])
+    with pytest.raises(ValueError):        # hidden size of another model
+        runner._validate([ForwardRequest("a", _Hidden(1, 128), h1.bundle.entries, runtime=cm,
+                                         handle=h1)])
+    hq = cm.create_handle("q", key_type="q8_0", value_type="q8_0")   # f16 pages, bf16 model
+    from pkv.modes import ModelCapabilityUnsupported
+    with pytest.raises(ModelCapabilityUnsupported):
+        runner._validate([ForwardRequest("q", _Hidden(1, 256), hq.bundle.entries, runtime=cm,
+                                         handle=hq)])
+    runner._validate([ok])
+    with pytest.raises(ValueError):
+        RunnerOutput(("a", "a"), (None, None), (1, 1))

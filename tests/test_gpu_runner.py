@@ -1,0 +1,148 @@
+"""GPU: ``PagedRunner.execute`` + ``CacheManager`` handles driving attention layers.
+
+A batch goes through prefill (ragged widths) and decode steps; every step's
+outputs are checked against a float32 restatement of the same layers on the
+CPU (projections rounded to the activation dtype as the GPU GEMMs do, RoPE,
+the history quantized and dequantized by the numpy oracle for q8_0 / q4_0
+caches, causal GQA attention by the oracle, output projection).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import numpy_ref
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pkv import _native
+
+    _native.load()
+
+
+def _rope(x, positions, inv_freq):
+    """x [H, T, D] float32, positions [T] -> rotate-half RoPE (float32)."""
+    ang = positions[None, :, None].astype(np.float32) * inv_freq[None, None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+    half = x.shape[-1] // 2
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate([a * cos - b * sin, b * cos + a * sin], -1).astype(np.float32)
+
+
+class Reference:
+    """float32 CPU restatement of the stack; keeps each request's K/V history."""
+
+    def __init__(self, model, bits, group, batch):
+        self.spec, self.bits, self.group = model.spec, bits, group
+        self.w = [(l.wq.float().cpu().numpy(), l.wk.float().cpu().numpy(),
+                   l.wv.float().cpu().numpy(), l.wo.float().cpu().numpy()) for l in model.layers]
+        self.inv = model.layers[0].inv_freq.cpu().numpy()
+        s = self.spec
+        self.k = [[np.zeros((s.kv_heads, 0, s.head_dim), np.float32) for _ in range(batch)]
+                  for _ in model.layers]
+        self.v = [[np.zeros((s.kv_heads, 0, s.head_dim), np.float32) for _ in range(batch)]
+                  for _ in model.layers]
+        self.round = (lambda a: a.astype(np.float16).astype(np.float32)) if s.dtype == "float16" \
+            else numpy_ref.bf16_round
+
+    def _seen(self, x):
+        if self.bits is None:
+            return x
+        return numpy_ref.dequantize_page(
+            numpy_ref.quantize_page(x.astype(np.float16), self.bits, self.group), self.bits,
+            x.shape[-1], self.group).astype(np.float32)
+
+    def step(self, hidden):
+        """hidden: list of [T_b, hidden] float32 -> list of outputs [T_b, hidden]."""
+        s = self.spec
+        xs = [self.round(h) for h in hidden]
+        for li, (wq, wk, wv, wo) in enumerate(self.w):
+            outs = []
+            for b, x in enumerate(xs):
+                t = x.shape[0]
+                start = self.k[li][b].shape[1]
+                pos = np.arange(start, start + t)
+                q = self.round(x @ wq).reshape(t, s.query_heads, s.head_dim).transpose(1, 0, 2)
+                k = self.round(x @ wk).reshape(t, s.kv_heads, s.head_dim).transpose(1, 0, 2)
+                v = self.round(x @ wv).reshape(t, s.kv_heads, s.head_dim).transpose(1, 0, 2)
+                q, k = self.round(_rope(q, pos, self.inv)), self.round(_rope(k, pos, self.inv))
+                self.k[li][b] = np.concatenate([self.k[li][b], self._seen(k)], 1)
+                self.v[li][b] = np.concatenate([self.v[li][b], self._seen(v)], 1)
+                att = numpy_ref.paged_attention(q[None], [self.k[li][b]], [self.v[li][b]],
+                                                [pos], [t], scale=1.0 / math.sqrt(s.head_dim))
+                att = self.round(att[0].astype(np.float32)).transpose(1, 0, 2).reshape(t, -1)
+                outs.append(self.round(att @ wo))
+            xs = outs
+        return xs
+
+
+def _close(got, want, max_rel, mean_rel):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    scale = float(np.abs(want).max()) + 1e-6
+    err = np.abs(got - want) / scale
+    assert np.isfinite(got).all()
+    assert err.max() <= max_rel, f"max rel error {err.max():.3e}"
+    assert err.mean() <= mean_rel, f"mean rel error {err.mean():.3e}"
+
+
+CASES = {
+    # name: (spec kwargs, key type, prefill widths, decode steps, block tokens, max_rel)
+    "small_f16": (dict(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                       dtype="float16"), "f16", (37, 5, 20), 3, 16, 2e-2),
+    "small_bf16": (dict(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                        dtype="bfloat16"), "bf16", (17, 33), 2, 32, 3e-2),
+    "small_q8": (dict(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                      dtype="float16"), "q8_0", (37, 5, 20), 3, 16, 2e-2),
+    "small_q4": (dict(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                      dtype="float16"), "q4_0", (24, 9), 2, 16, 4e-2),
+    "llama3_8b_layer_q8": (dict(num_layers=1, dtype="float16"), "q8_0", (40, 3), 2, 16, 2e-2),
+}
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_runner_prefill_then_decode_matches_reference(case):
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    kw, key_type, prefill, steps, block, max_rel = CASES[case]
+    spec = ModelSpec(**kw)
+    model = AttentionStack(spec, seed=3)
+    cm = CacheManager(model, CacheConfig(block_size_tokens=block, key_type=key_type,
+                                         value_type=key_type, memory_budget_bytes=1 << 30))
+    handles = [cm.create_handle(f"r{i}", key_type=key_type, value_type=key_type)
+               for i in range(len(prefill))]
+    bits = {"q8_0": 8, "q4_0": 4}.get(key_type)
+    ref = Reference(model, bits, 32, len(prefill))
+    runner = PagedRunner(model)
+    rng = np.random.default_rng(11)
+    dtype = getattr(torch, spec.dtype)
+    widths_seq = [prefill] + [(1,) * len(prefill)] * steps
+    for step, widths in enumerate(widths_seq):
+        hidden = [rng.standard_normal((w, spec.hidden)).astype(np.float32) for w in widths]
+        reqs = [ForwardRequest(h.request_id, torch.from_numpy(x).to("cuda", dtype),
+                               h.bundle.entries, phase="prefill" if step == 0 else "decode",
+                               runtime=cm, handle=h, return_all_logits=step == 0)
+                for h, x in zip(handles, hidden)]
+        out = runner.execute(reqs)
+        want = ref.step(hidden)
+        assert out.committed_token_counts == tuple(widths)
+        for i, w in enumerate(widths):
+            got = out.logits[i][0].float().cpu().numpy()
+            _close(got, want[i][-got.shape[0]:], max_rel, max_rel / 10)
+        offsets = [sum(ws[i] for ws in widths_seq[:step + 1]) for i in range(len(prefill))]
+        assert [h.token_count for h in handles] == offsets
+        assert [h.bundle.offset for h in handles] == offsets
+    for h in handles:
+        cm.release(h)
+    assert cm.stats().live_handles == 0
