@@ -126,8 +126,10 @@ class AttentionLayer:
         return apply_rope(q, positions, self.inv_freq), apply_rope(k, positions, self.inv_freq), v
 
     def __call__(self, x, cache, position_ids):
-        """One layer through ``cache.attend`` (``transformer.py:202-209``)."""
-        q, k, v = self.project(x, position_ids)
+        """One layer through ``cache.attend`` (``transformer.py:202-209``).  Host
+        ``position_ids`` stay on the host for the cache's position check (no
+        device sync); RoPE reads a device copy."""
+        q, k, v = self.project(x, position_ids.to(x.device, non_blocking=True))
         out = cache.attend(q.contiguous(), k.contiguous(), v.contiguous(), scale=self.scale,
                            position_ids=position_ids)
         batch, _, width, _ = out.shape

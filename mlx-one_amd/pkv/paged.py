@@ -202,6 +202,29 @@ class PagedKVCache:
         for ref in old:
             ref.close()
 
+    def checkpoint(self):
+        """State an in-place append can be rolled back to (see ``rollback``)."""
+        tail = self._blocks[-1].block if self._blocks else None
+        return (len(self._blocks), self._offset, tail,
+                tail.token_count if tail is not None else 0,
+                tail.immutable if tail is not None else False)
+
+    def rollback(self, mark):
+        """Undo appends made since ``checkpoint()``: pages taken since are
+        released, the tail page gets back its token count (and its mutability,
+        if the undone append filled and sealed it), the page table its length.
+        Bytes written past the restored count are never read."""
+        count, offset, tail, tail_tokens, sealed = mark
+        while len(self._blocks) > count:
+            self._blocks.pop().close()
+        if tail is not None:
+            tail.token_count = tail_tokens
+            tail.immutable = sealed
+        self._offset = offset
+        self.page_table.truncate(count)
+        if count:
+            self.page_table.update(count - 1, self._blocks[-1])
+
     def reset(self):
         for ref in self._blocks:
             ref.close()
@@ -265,7 +288,7 @@ class PagedBatchCache:
             for row, (cache, real) in enumerate(zip(self.rows, self.widths, strict=True)):
                 expected[row, :real] = torch.arange(cache.offset, cache.offset + real)
                 mask[row, :real] = True
-            given = position_ids.to("cpu", torch.int64)
+            given = position_ids.to("cpu", torch.int64)  # free for host tensors
             if not bool((given[mask] == expected[mask]).all()):
                 raise ValueError("paged query logical positions mismatch")
         positions = [tuple(range(c.offset, c.offset + width)) for c in self.rows]

@@ -1,16 +1,20 @@
 """``PagedRunner.execute``: a batch step over paged caches (``engine/paged.py:285-417``).
 
-Same flow and checks as the reference, with this build's attention stack as
-the model: validate the batch (same model, phase, layer count; every cache a
+Same checks as the reference, with this build's attention stack as the
+model: validate the batch (same model, phase, layer count; every cache a
 ``PagedKVCache`` of its layer in the model's activation dtype; one pool and
-precision), reserve the step's transient bytes on the cache manager, **clone**
-every layer cache (sealed pages shared, mutable tails copied: the drafts),
-run the layers over ``PagedBatchCache`` views of the drafts (append +
-attention per layer), pick each request's outputs (all positions for
-``return_all_logits``, else the last), then **commit** the drafts into the
-request caches and release the rest.  A failure anywhere leaves the request
-caches untouched.  Requests carry hidden states ``[T, hidden]`` where the
-reference carries token ids: embedding and LM head sit outside the path.
+precision), reserve the step's transient bytes on the cache manager, run the
+layers over ``PagedBatchCache`` views (append + attention per layer), pick
+each request's outputs (all positions for ``return_all_logits``, else the
+last).  A failure anywhere leaves the request caches as they were.
+
+Two ways to get that guarantee: the reference's (``copy_on_write=True``:
+clone every layer cache -- sealed pages shared, mutable tails copied -- run on
+the clones and commit them, :377-403), and the default: append in place and,
+on failure, roll every cache back to its checkpoint by length (pages taken
+released, tail counts restored), which saves the per-step tail copies.
+Requests carry hidden states ``[T, hidden]`` where the reference carries
+token ids: embedding and LM head sit outside the path.
 """
 
 from __future__ import annotations
@@ -61,8 +65,9 @@ class RunnerOutput:
 
 
 class PagedRunner:
-    def __init__(self, model):
+    def __init__(self, model, *, copy_on_write=False):
         self.model = model
+        self.copy_on_write = copy_on_write
         self.last_trace = {}
 
     def _validate(self, requests):
@@ -114,38 +119,53 @@ class PagedRunner:
         transient = len(requests) * width * spec.num_layers * 4 * (
             spec.hidden + (spec.query_heads + 2 * spec.kv_heads) * spec.head_dim) * 2
         runtime = first.runtime
-        drafts = []
+        device = first.hidden.device
+        x = torch.zeros((len(requests), width, spec.hidden), dtype=first.hidden.dtype,
+                        device=device)
+        positions = torch.zeros((len(requests), width), dtype=torch.int64)
+        for i, r in enumerate(requests):
+            x[i, :widths[i]] = r.hidden
+            start = r.cache[0].offset
+            positions[i, :widths[i]] = torch.arange(start, start + widths[i])
         outputs = []
+
+        def run(rows):
+            packed = tuple(PagedBatchCache(tuple(row[layer] for row in rows), widths, metrics)
+                           for layer in range(len(first.cache)))
+            y = self.model.forward(x, cache=packed, position_ids=positions)
+            for i, n in enumerate(widths):
+                begin = 0 if requests[i].return_all_logits else n - 1
+                outputs.append(y[i:i + 1, begin:n].clone())
+
         with ExitStack() as stack:
             if runtime is not None:
                 stack.enter_context(runtime.transient_reservation(transient))
-            try:
-                for r in requests:
-                    drafts.append([c.clone() for c in r.cache])
-                packed = tuple(PagedBatchCache(tuple(d[layer] for d in drafts), widths, metrics)
-                               for layer in range(len(first.cache)))
-                device = first.hidden.device
-                x = torch.zeros((len(requests), width, spec.hidden), dtype=first.hidden.dtype,
-                                device=device)
-                positions = torch.zeros((len(requests), width), dtype=torch.int64)
-                for i, r in enumerate(requests):
-                    x[i, :widths[i]] = r.hidden
-                    start = r.cache[0].offset
-                    positions[i, :widths[i]] = torch.arange(start, start + widths[i])
-                y = self.model.forward(x, cache=packed, position_ids=positions.to(device))
-                for i, n in enumerate(widths):
-                    begin = 0 if requests[i].return_all_logits else n - 1
-                    outputs.append(y[i:i + 1, begin:n].clone())
-                # commit: the drafts become the request caches (old refs closed)
-                for r, layers in zip(requests, drafts, strict=True):
-                    for cache, draft in zip(r.cache, layers, strict=True):
-                        cache.replace_from(draft)
-                    if r.handle is not None:
-                        r.handle.token_count = r.cache[0].offset
-            finally:
-                for layers in drafts:
-                    for draft in layers:
-                        draft.reset()   # no-op for committed drafts (emptied by replace_from)
+            if self.copy_on_write:
+                drafts = []
+                try:
+                    for r in requests:
+                        drafts.append([c.clone() for c in r.cache])
+                    run(drafts)
+                    # commit: the drafts become the request caches (old refs closed)
+                    for r, layers in zip(requests, drafts, strict=True):
+                        for cache, draft in zip(r.cache, layers, strict=True):
+                            cache.replace_from(draft)
+                finally:
+                    for layers in drafts:
+                        for draft in layers:
+                            draft.reset()   # no-op for committed drafts (emptied by replace_from)
+            else:
+                marks = [[c.checkpoint() for c in r.cache] for r in requests]
+                try:
+                    run([r.cache for r in requests])
+                except BaseException:
+                    for r, layer_marks in zip(requests, marks, strict=True):
+                        for cache, mark in zip(r.cache, layer_marks, strict=True):
+                            cache.rollback(mark)
+                    raise
+            for r in requests:
+                if r.handle is not None:
+                    r.handle.token_count = r.cache[0].offset
         self.last_trace = {**metrics, "phase": first.phase,
                            "request_ids": [r.request_id for r in requests],
                            "batch_size": len(requests),

@@ -119,3 +119,26 @@ def test_runner_rejects_inconsistent_batches():
     runner._validate([ok])
     with pytest.raises(ValueError):
         RunnerOutput(("a", "a"), (None, None), (1, 1))
+
+
+def test_in_place_append_rolls_back_by_length():
+    """checkpoint / rollback undo page allocation, tail fill and sealing."""
+    cm = _manager(block_size_tokens=16)
+    h = cm.create_handle("r", key_type="bf16", value_type="bf16")
+    cache = h.bundle.entries[0]
+    layout = cache.layout_for(2, 64)
+    cache._plan_append(10, layout)               # one partial page
+    before_pages = list(cache.page_table.pages)
+    live_before = cm.block_pool.stats()["block_live"]
+    mark = cache.checkpoint()
+    cache._plan_append(40, layout)               # fills + seals the tail, two more pages
+    assert cache.offset == 50 and len(cache._blocks) == 4
+    assert cache._blocks[0].block.immutable
+    cache.rollback(mark)
+    assert cache.offset == 10 and len(cache._blocks) == 1
+    tail = cache._blocks[0].block
+    assert tail.token_count == 10 and not tail.immutable
+    assert list(cache.page_table.pages) == before_pages
+    assert cm.block_pool.stats()["block_live"] == live_before
+    cache._plan_append(6, layout)                # appends continue from the restored tail
+    assert cache.offset == 16 and cache._blocks[0].block.immutable

@@ -109,8 +109,9 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("copy_on_write", [False, True])
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_runner_prefill_then_decode_matches_reference(case):
+def test_runner_prefill_then_decode_matches_reference(case, copy_on_write):
     from pkv.cache_manager import CacheConfig, CacheManager
     from pkv.layer import AttentionStack, ModelSpec
     from pkv.runner import ForwardRequest, PagedRunner
@@ -124,7 +125,7 @@ def test_runner_prefill_then_decode_matches_reference(case):
                for i in range(len(prefill))]
     bits = {"q8_0": 8, "q4_0": 4}.get(key_type)
     ref = Reference(model, bits, 32, len(prefill))
-    runner = PagedRunner(model)
+    runner = PagedRunner(model, copy_on_write=copy_on_write)
     rng = np.random.default_rng(11)
     dtype = getattr(torch, spec.dtype)
     widths_seq = [prefill] + [(1,) * len(prefill)] * steps
@@ -146,3 +147,57 @@ def test_runner_prefill_then_decode_matches_reference(case):
     for h in handles:
         cm.release(h)
     assert cm.stats().live_handles == 0
+
+
+class _FailAfterFirstLayer:
+    """A stack that raises after its first layer has appended and attended."""
+
+    def __init__(self, model):
+        self.model, self.spec, self.activation_dtype = model, model.spec, model.activation_dtype
+
+    def forward(self, x, *, cache, position_ids):
+        self.model.layers[0](x, cache[0], position_ids)
+        raise RuntimeError("planted failure")
+
+
+@pytest.mark.parametrize("copy_on_write", [False, True])
+def test_failed_step_leaves_caches_unchanged(copy_on_write):
+    """A step that fails mid-way rolls back (or drops its clones); the next step
+    matches a reference that never saw it."""
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, seed=5)
+    cm = CacheManager(model, CacheConfig(block_size_tokens=16, key_type="q8_0",
+                                         value_type="q8_0"))
+    handles = [cm.create_handle(f"r{i}", key_type="q8_0", value_type="q8_0") for i in range(2)]
+    ref = Reference(model, 8, 32, 2)
+    good, bad = PagedRunner(model, copy_on_write=copy_on_write), PagedRunner(
+        _FailAfterFirstLayer(model), copy_on_write=copy_on_write)
+    rng = np.random.default_rng(5)
+
+    def requests(widths, phase):
+        hidden = [rng.standard_normal((w, spec.hidden)).astype(np.float32) for w in widths]
+        return hidden, [ForwardRequest(h.request_id, torch.from_numpy(x).to("cuda", torch.float16),
+                                       h.bundle.entries, phase=phase, runtime=cm, handle=h)
+                        for h, x in zip(handles, hidden)]
+
+    hidden, reqs = requests((15, 16), "prefill")   # a partial page and a page just filled
+    good.execute(reqs)
+    ref.step(hidden)
+    state = [[(c.offset, len(c._blocks), list(c.page_table.pages)) for c in h.bundle.entries]
+             for h in handles]
+    _, reqs = requests((1, 1), "decode")
+    with pytest.raises(RuntimeError, match="planted failure"):
+        bad.execute(reqs)
+    assert [[(c.offset, len(c._blocks), list(c.page_table.pages)) for c in h.bundle.entries]
+            for h in handles] == state
+    assert [h.token_count for h in handles] == [15, 16]
+    hidden, reqs = requests((1, 1), "decode")
+    out = good.execute(reqs)
+    want = ref.step(hidden)
+    for i in range(2):
+        _close(out.logits[i][0].float().cpu().numpy(), want[i][-1:], 2e-2, 2e-3)
