@@ -237,6 +237,85 @@ def workload_waves(w, lengths):
     return max(1, -(-tiles * 16 // w.split_tokens))
 
 
+def layer_bench(args):
+    """End to end through ``PagedRunner.execute``: decode steps of one Llama-3-8B
+    attention layer (q/k/v projections, RoPE, append + paged attention in
+    libpkv, output projection) for C2's batch and context lengths, q8_0 KV
+    (f16 activations, as the reference's CacheManager pairs q8_0 with f16).
+    Contexts are prefilled through the runner in 1,024-token chunks before
+    timing; each timed step is one runner call (host bookkeeping included)."""
+    import numpy as np
+    import torch
+
+    from pkv import _native, workloads
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    _native.load()
+    device = torch.device("cuda:0")
+    w = workloads.get("c2")
+    inst = workloads.generate(w, kv=False)
+    spec = ModelSpec(hidden=4096, query_heads=w.heads, kv_heads=w.kv_heads, head_dim=w.head_dim,
+                     num_layers=1, dtype="float16")
+    model = AttentionStack(spec, device=device, seed=w.seed)
+    cm = CacheManager(model, CacheConfig(block_size_tokens=w.page_tokens, key_type="q8_0",
+                                         value_type="q8_0", group_size=w.group_size,
+                                         memory_budget_bytes=64 << 30), device=device)
+    handles = [cm.create_handle(f"seq{b}", key_type="q8_0", value_type="q8_0")
+               for b in range(w.batch)]
+    runner = PagedRunner(model)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    context = [int(x) for x in inst.context]
+
+    def step(widths, phase, hidden=None):
+        if hidden is None:
+            hidden = [torch.randn((n, spec.hidden), generator=gen, device=device,
+                                  dtype=torch.float16) for n in widths]
+        reqs = [ForwardRequest(h.request_id, x, h.bundle.entries, phase=phase, runtime=cm,
+                               handle=h)
+                for h, n, x in zip(handles, widths, hidden) if n > 0]
+        return runner.execute(reqs)
+
+    chunk = 1024
+    while True:
+        left = [c - h.token_count for c, h in zip(context, handles)]
+        if max(left) <= 0:
+            break
+        # rows with nothing left to prefill sit the chunk out
+        step([min(chunk, max(n, 0)) for n in left], "prefill")
+    # decode inputs are generated before timing: [step][row] -> [1, hidden]
+    decode_in = torch.randn((args.warmup + args.steps, w.batch, 1, spec.hidden), generator=gen,
+                            device=device, dtype=torch.float16).unbind(0)
+    decode_in = [x.unbind(0) for x in decode_in]
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        step([1] * w.batch, "decode", decode_in[i])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step([1] * w.batch, "decode", decode_in[args.warmup + i])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    trace = runner.last_trace
+    result = {
+        "metric": "e2e attention-layer decode tok/s (PagedRunner, Llama-3-8B layer, q8_0 KV)",
+        "value": round(w.batch / (ms / 1e3), 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "layer", "batch": w.batch, "hidden": spec.hidden,
+                   "heads": spec.query_heads, "kv_heads": spec.kv_heads,
+                   "head_dim": spec.head_dim, "kv": "q8_0", "group_size": w.group_size,
+                   "page_tokens": w.page_tokens,
+                   "mean_context": float(np.mean([h.token_count for h in handles]))},
+        "host_dispatch_ms_last_step": round(trace.get("synchronized_kernel_dispatch_ms", 0.0), 4),
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -257,6 +336,11 @@ def main(argv=None):
     args = parser.parse_args(argv)
     if args.copy_probe:
         return copy_probe()
+    if args.workload == "layer":
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+            return 2
+        return layer_bench(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the paged decode path "
                           "shards by sequence with no exchange; run with --gpus 1"}))

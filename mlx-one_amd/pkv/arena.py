@@ -15,6 +15,8 @@ from __future__ import annotations
 import weakref
 from contextlib import contextmanager
 
+import numpy as np
+
 from pkv.block_cache import BlockPool
 from pkv.cache_errors import CacheCapacityError, CacheCorruptionError
 
@@ -192,11 +194,14 @@ class PersistentPageTable:
     token_count)`` tuples; chunks are immutable tuples shared by forks, and
     an edit replaces one chunk (accounted as 256 bytes, as the reference's
     ``[16, 4]`` int32 chunk).  ``pages`` lists the pool page ids in order --
-    the row of the device block table.
+    the row of the device block table, also kept as an int32 array (``row()``)
+    so a batch table is assembled by slice copies.  Forks copy ``entries``,
+    so edits mutate it in place.
     """
 
     def __init__(self, arena):
         self.arena, self.chunks, self.entries, self.pages = arena, {}, {}, []
+        self._ids = np.full(SEGMENT_PAGES, -1, np.int32)
         arena._tables.add(self)
 
     @property
@@ -207,7 +212,12 @@ class PersistentPageTable:
         result = PersistentPageTable(self.arena)
         result.chunks, result.entries, result.pages = dict(self.chunks), dict(self.entries), list(
             self.pages)
+        result._ids = self._ids.copy()
         return result
+
+    def row(self):
+        """``pages`` as an int32 array view (valid until the next edit)."""
+        return self._ids[:len(self.pages)]
 
     def _rebuild_chunk(self, chunk):
         self.chunks[chunk] = tuple(self.entries.get(i, (-1, -1, 0, 0))
@@ -220,16 +230,29 @@ class PersistentPageTable:
         entry = (sid, slot, index * self.arena.block_tokens, block.token_count)
         if self.entries.get(index) == entry:
             return
-        self.entries = {**self.entries, index: entry}
+        self.entries[index] = entry
+        chunk = index // SEGMENT_PAGES
+        if chunk in self.chunks:    # edit one slot of the chunk
+            row = list(self.chunks[chunk])
+            row[index % SEGMENT_PAGES] = entry
+            self.chunks[chunk] = tuple(row)
+            self.arena.table_update_bytes += SEGMENT_PAGES * 4 * 4
+        else:
+            self._rebuild_chunk(chunk)
         while len(self.pages) <= index:
             self.pages.append(-1)
         self.pages[index] = block.page
-        self._rebuild_chunk(index // SEGMENT_PAGES)
+        if index >= len(self._ids):
+            grown = np.full(max(2 * len(self._ids), index + 1), -1, np.int32)
+            grown[:len(self._ids)] = self._ids
+            self._ids = grown
+        self._ids[index] = block.page
 
     def truncate(self, length):
         for index in [i for i in self.entries if i >= length]:
             del self.entries[index]
         del self.pages[length:]
+        self._ids[length:] = -1
         for chunk in list(self.chunks):
             if chunk * SEGMENT_PAGES >= length:
                 del self.chunks[chunk]

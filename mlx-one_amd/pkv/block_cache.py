@@ -118,6 +118,7 @@ class BlockPool:
         self._epoch = uuid.uuid4().int
         self._generation = 0
         self._lock = threading.RLock()
+        self._live_nbytes = 0      # sum of nbytes over live blocks, kept incrementally
 
     # -- identities --------------------------------------------------------
     def _identity(self, slot):
@@ -139,11 +140,13 @@ class BlockPool:
             block_id = self._identity(page)
             self._blocks[block_id] = CacheBlock(block_id, token_count, page=page, layout=layout,
                                                 nbytes=nbytes)
+            self._live_nbytes += nbytes
             if state is not None:
                 try:
                     self._store_state(self._blocks[block_id], state)
                 except BaseException:
                     del self._blocks[block_id]
+                    self._live_nbytes -= nbytes
                     self._reclaim_page(layout, page)
                     raise
             return block_id
@@ -190,13 +193,14 @@ class BlockPool:
 
     def _drop(self, block):
         del self._blocks[block.block_id]
+        self._live_nbytes -= block.nbytes
         self._reclaim_page(block.layout, block.page)
 
     # -- accounting ------------------------------------------------------------
     @property
     def nbytes(self):
         with self._lock:
-            return sum(b.nbytes for b in self._blocks.values())
+            return self._live_nbytes
 
     def stats(self):
         with self._lock:
@@ -223,6 +227,7 @@ class BlockPool:
     def clear(self):
         with self._lock:
             self._blocks.clear()
+            self._live_nbytes = 0
             self._next_id = 0
             self._epoch = uuid.uuid4().int
 

@@ -18,6 +18,7 @@ codes, scales and biases.  Clone copies the mutable tail page on the device.
 
 from __future__ import annotations
 
+import functools
 import math
 import time
 
@@ -53,6 +54,15 @@ def dequantize_page(state, bits, dim, group_size=32):
     return ops.dequantize_rows(state, bits, dim, group_size)
 
 
+@functools.lru_cache(maxsize=256)
+def _layout(layer_id, page_tokens, heads, dim, dtype, bits, group_size):
+    """One shared ``BlockLayout`` object per distinct page format (identity compares)."""
+    return BlockLayout(version=3, layer_id=layer_id, page_tokens=page_tokens,
+                       num_kv_heads=heads, head_dim=dim, key_dtype=dtype, value_dtype=dtype,
+                       quantization_bits=bits, quantization_group_size=group_size,
+                       kernel_version=KERNEL_VERSION)
+
+
 class PagedKVCache:
     """One layer of one sequence: page refs, offset and a persistent page table."""
 
@@ -83,11 +93,8 @@ class PagedKVCache:
         return tuple(r for r in self._blocks if r.block.token_count == self.block_tokens)
 
     def layout_for(self, heads, dim):
-        return BlockLayout(version=3, layer_id=self.layer_id, page_tokens=self.block_tokens,
-                           num_kv_heads=int(heads), head_dim=int(dim), key_dtype=self.dtype,
-                           value_dtype=self.dtype, quantization_bits=self.bits,
-                           quantization_group_size=self.group_size,
-                           kernel_version=KERNEL_VERSION)
+        return _layout(self.layer_id, self.block_tokens, int(heads), int(dim), self.dtype,
+                       self.bits, self.group_size)
 
     @property
     def layout(self):
@@ -100,8 +107,10 @@ class PagedKVCache:
     # -- host page bookkeeping ------------------------------------------------------
     def _plan_append(self, width, layout):
         """Reserve pages and advance counts for ``width`` new tokens; returns start offset."""
-        if self._blocks and self._blocks[0].block.layout != layout:
-            raise ValueError("paged append layout mismatch")
+        if self._blocks:
+            stored = self._blocks[0].block.layout
+            if stored is not layout and stored != layout:
+                raise ValueError("paged append layout mismatch")
         start = self._offset
         cursor = 0
         while cursor < width:
@@ -125,7 +134,7 @@ class PagedKVCache:
     def page_row(self, width):
         """Page ids of this sequence, padded with -1 to ``width`` entries."""
         row = np.full(width, -1, np.int32)
-        pages = self.page_table.pages
+        pages = self.page_table.row()
         row[:len(pages)] = pages
         return row
 
@@ -280,34 +289,48 @@ class PagedBatchCache:
         from pkv.paged_attention import paged_attention
 
         batch, _, width, _ = queries.shape
+        offsets = np.array([cache.offset for cache in self.rows], np.int64)
+        widths = np.array(self.widths, np.int64)
+        # logical positions of every query column (padding columns continue the row)
+        positions = offsets[:, None] + np.arange(width)[None, :]
         if position_ids is not None:
             if tuple(position_ids.shape) != (len(self.rows), width):
                 raise ValueError("paged query position shape mismatch")
-            expected = torch.zeros((batch, width), dtype=torch.int64)
-            mask = torch.zeros((batch, width), dtype=torch.bool)
-            for row, (cache, real) in enumerate(zip(self.rows, self.widths, strict=True)):
-                expected[row, :real] = torch.arange(cache.offset, cache.offset + real)
-                mask[row, :real] = True
-            given = position_ids.to("cpu", torch.int64)  # free for host tensors
-            if not bool((given[mask] == expected[mask]).all()):
+            mask = np.arange(width)[None, :] < widths[:, None]
+            given = position_ids.to("cpu", torch.int64).numpy()  # free for host tensors
+            if not bool((given[mask] == positions[mask]).all()):
                 raise ValueError("paged query logical positions mismatch")
-        positions = [tuple(range(c.offset, c.offset + width)) for c in self.rows]
         # host: pages for every row, then one append launch for the whole batch
         layout = self.rows[0].layout_for(keys.shape[1], keys.shape[3])
         starts = [cache._plan_append(real, layout)
                   for cache, real in zip(self.rows, self.widths, strict=True)]
         pool = self.rows[0].pool.pool_for(layout)
         device = pool.buffer.device
+        # the step's int32 metadata in one pinned buffer and one host->device copy:
+        # block table [B, pages] | start [B] | width [B] | length [B] | q_pos [B, width]
         max_pages = max(len(c.page_table.pages) for c in self.rows)
-        table = torch.from_numpy(np.stack([c.page_row(max_pages) for c in self.rows])).to(device)
+        sizes = (batch * max_pages, batch, batch, batch, batch * width)
+        host = torch.empty(sum(sizes), dtype=torch.int32, pin_memory=device.type == "cuda")
+        parts = np.split(host.numpy(), np.cumsum(sizes)[:-1])
+        table_h = parts[0].reshape(batch, max_pages)
+        table_h.fill(-1)
+        for row, cache in enumerate(self.rows):
+            ids = cache.page_table.row()
+            table_h[row, :len(ids)] = ids
+        parts[1][:] = starts
+        parts[2][:] = widths
+        parts[3][:] = [cache.offset for cache in self.rows]
+        parts[4][:] = positions.reshape(-1)
+        meta = host.to(device, non_blocking=True)
+        table, start_d, width_d, length_d, qpos_d = torch.split(meta, sizes)
+        table = table.view(batch, max_pages)
         dtype = _torch_dtype(self.rows[0].dtype)
         ops.append_quantize(pool.fmt, pool.buffer, keys.to(device, dtype).contiguous(),
-                            values.to(device, dtype).contiguous(), table,
-                            torch.tensor(starts, dtype=torch.int32, device=device),
-                            torch.tensor(list(self.widths), dtype=torch.int32, device=device))
+                            values.to(device, dtype).contiguous(), table, start_d, width_d)
         started = time.perf_counter()
-        result = paged_attention(queries, self.rows, positions, self.widths, scale=scale,
-                                 _table=table)
+        result = paged_attention(queries, self.rows, positions.tolist(), self.widths,
+                                 scale=scale,
+                                 _device_meta=(table, length_d, qpos_d.view(batch, width), width_d))
         self.metrics["synchronized_kernel_dispatch_ms"] = self.metrics.get(
             "synchronized_kernel_dispatch_ms", 0.0) + (time.perf_counter() - started) * 1000
         self.metrics["direct_attention_calls"] = self.metrics.get("direct_attention_calls", 0) + 1

@@ -45,7 +45,9 @@ def page_bindings(rows):
     return np.stack([c.page_row(max(longest, 1)) for c in rows])
 
 
-def paged_attention(queries, rows, positions, widths, *, scale, _table=None):
+def paged_attention(queries, rows, positions, widths, *, scale, _device_meta=None):
+    """``_device_meta``: ``(block_table, lengths, q_pos, widths)`` already on the
+    device, from a caller that has just written them (``PagedBatchCache.attend``)."""
     import torch
 
     from pkv import ops
@@ -64,20 +66,18 @@ def paged_attention(queries, rows, positions, widths, *, scale, _table=None):
         raise ValueError("batch spans page arenas")
     if any(c._blocks[0].block.layout != layout for c in rows):
         raise ModelCapabilityUnsupported("incompatible arena page layouts")
-    table = page_bindings(rows) if _table is None else None
     pool = arena.pool_for(layout)
     with arena.lease():
         device = pool.buffer.device
-        if _table is None:
-            _table = torch.from_numpy(table).to(device)
-        lengths = [c.offset for c in rows]
+        if _device_meta is None:
+            table = torch.from_numpy(page_bindings(rows)).to(device)
+            lengths = torch.tensor([c.offset for c in rows], dtype=torch.int32, device=device)
+            q_pos = torch.tensor([list(p) for p in positions], dtype=torch.int32, device=device)
+            width_d = torch.tensor(list(widths), dtype=torch.int32, device=device)
+        else:
+            table, lengths, q_pos, width_d = _device_meta
         dtype = queries.dtype
         q = queries.to(device, pool.fmt.dtype)
-        out = ops.paged_attention(pool.fmt, pool.buffer, q, _table,
-                                  torch.tensor(lengths, dtype=torch.int32, device=device),
-                                  scale=scale,
-                                  q_pos=torch.tensor([list(p) for p in positions], dtype=torch.int32,
-                                                     device=device),
-                                  widths=torch.tensor(list(widths), dtype=torch.int32,
-                                                      device=device))
+        out = ops.paged_attention(pool.fmt, pool.buffer, q, table, lengths, scale=scale,
+                                  q_pos=q_pos, widths=width_d)
         return out.to(dtype)

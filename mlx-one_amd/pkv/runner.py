@@ -23,6 +23,8 @@ import time
 from contextlib import ExitStack
 from dataclasses import dataclass
 
+import numpy as np
+
 from pkv.modes import ModelCapabilityUnsupported
 from pkv.paged import KERNEL_VERSION, PagedBatchCache, PagedKVCache
 
@@ -93,11 +95,12 @@ class PagedRunner:
             for cache, layout in zip(r.cache, layers, strict=True):
                 if cache.dtype != self.model.activation_dtype:
                     raise ModelCapabilityUnsupported("paged storage differs from execution precision")
-                for reference in cache._blocks:
-                    stored = reference.block.layout
-                    if (stored.num_kv_heads != layout.kv_heads or stored.head_dim != layout.key_dim
-                            or stored.layer_id != layout.layer_id):
-                        raise ValueError("paged layer layout differs from the model")
+                # one layout per cache (append and adopt enforce it): its first page's
+                stored = cache.layout
+                if stored is not None and (stored.num_kv_heads != layout.kv_heads
+                                           or stored.head_dim != layout.key_dim
+                                           or stored.layer_id != layout.layer_id):
+                    raise ValueError("paged layer layout differs from the model")
         if len({(id(c.pool), c.dtype, c.bits) for r in requests for c in r.cache}) != 1:
             raise ValueError("incompatible paged pools or precision")
         if any(r.runtime is not first.runtime for r in requests):
@@ -120,22 +123,31 @@ class PagedRunner:
             spec.hidden + (spec.query_heads + 2 * spec.kv_heads) * spec.head_dim) * 2
         runtime = first.runtime
         device = first.hidden.device
-        x = torch.zeros((len(requests), width, spec.hidden), dtype=first.hidden.dtype,
-                        device=device)
-        positions = torch.zeros((len(requests), width), dtype=torch.int64)
-        for i, r in enumerate(requests):
-            x[i, :widths[i]] = r.hidden
-            start = r.cache[0].offset
-            positions[i, :widths[i]] = torch.arange(start, start + widths[i])
+        if all(n == width for n in widths) and all(
+                r.hidden.dtype == first.hidden.dtype and r.hidden.device == device
+                for r in requests):
+            x = torch.stack([r.hidden for r in requests])          # one copy kernel
+        else:
+            x = torch.zeros((len(requests), width, spec.hidden), dtype=first.hidden.dtype,
+                            device=device)
+            for i, r in enumerate(requests):
+                x[i, :widths[i]] = r.hidden
+        # logical positions (padding columns continue the row), pinned so RoPE's
+        # device copy does not stall the host
+        positions = torch.empty((len(requests), width), dtype=torch.int64,
+                                pin_memory=device.type == "cuda")
+        starts = np.array([r.cache[0].offset for r in requests], np.int64)
+        positions.numpy()[:] = starts[:, None] + np.arange(width)[None, :]
         outputs = []
 
         def run(rows):
             packed = tuple(PagedBatchCache(tuple(row[layer] for row in rows), widths, metrics)
                            for layer in range(len(first.cache)))
             y = self.model.forward(x, cache=packed, position_ids=positions)
+            # views of this step's fresh output tensor
             for i, n in enumerate(widths):
                 begin = 0 if requests[i].return_all_logits else n - 1
-                outputs.append(y[i:i + 1, begin:n].clone())
+                outputs.append(y[i:i + 1, begin:n])
 
         with ExitStack() as stack:
             if runtime is not None:
