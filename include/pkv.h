@@ -168,6 +168,22 @@ int pkv_quantize_rows(void *stream, const void *values, int64_t rows, int32_t di
 int pkv_dequantize_rows(void *stream, const void *codes, const void *scale, const void *bias,
                         int64_t rows, int32_t dim, int32_t bits, int32_t group_size, void *out);
 
+/*
+ * Caller side of the attend: rotate-half RoPE of a fused projection
+ * qkv [batch][tokens][heads + 2*kv_heads][dim] (float_kind values) at
+ * positions [batch][tokens] with inv_freq [dim/2] (float32), written
+ * head-major: q [batch][heads][tokens][dim] rotated, k [batch][kv_heads][tokens][dim]
+ * rotated, v [batch][kv_heads][tokens][dim] copied.  Per element:
+ * angle = f32(pos) * inv_freq[i], out = (a*cos - b*sin, b*cos + a*sin) with
+ * each product and sum rounded in float32, then one RNE cast.  Replaces the
+ * projection split and apply_rotary_pos_emb of the reference's attention block
+ * (src/mlx_one/models/shared/transformer.py:32-90, :146-184), which feeds
+ * PagedBatchCache.attend.  dim even, at most 256.
+ */
+int pkv_rope_qkv(void *stream, const void *qkv, int32_t batch, int32_t tokens, int32_t heads,
+                 int32_t kv_heads, int32_t dim, int32_t float_kind, const int32_t *positions,
+                 const float *inv_freq, void *q, void *k, void *v);
+
 #ifdef __cplusplus
 }
 #endif

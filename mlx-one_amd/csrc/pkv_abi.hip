@@ -341,3 +341,29 @@ int pkv_dequantize_rows(void *stream, const void *codes, const void *scale, cons
 }
 
 }  // extern "C"
+
+int pkv_rope_qkv(void *stream, const void *qkv, int32_t batch, int32_t tokens, int32_t heads,
+                 int32_t kv_heads, int32_t dim, int32_t float_kind, const int32_t *positions,
+                 const float *inv_freq, void *q, void *k, void *v) {
+  if (float_kind != 0 && float_kind != 1) return fail(PKV_INVALID_ARGUMENT, "float_kind must be 0 or 1");
+  if (batch < 0 || tokens < 0 || heads < 1 || kv_heads < 1 || dim < 2 || dim > 256 || (dim & 1))
+    return fail(PKV_INVALID_ARGUMENT, "invalid RoPE shape");
+  if ((int64_t)batch * tokens == 0) return PKV_OK;
+  if ((int64_t)batch * tokens > 0x7fffffff) return fail(PKV_INVALID_ARGUMENT, "too many RoPE rows");
+  if (!qkv || !positions || !inv_freq || !q || !k || !v)
+    return fail(PKV_INVALID_ARGUMENT, "NULL tensor");
+  pkv::RopeArgs a;
+  a.qkv = (const uint16_t *)qkv;
+  a.rows = (int64_t)batch * tokens;
+  a.tokens = tokens;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.dim = dim;
+  a.float_kind = float_kind;
+  a.positions = positions;
+  a.inv_freq = inv_freq;
+  a.q = (uint16_t *)q;
+  a.k = (uint16_t *)k;
+  a.v = (uint16_t *)v;
+  return check_launch(pkv::launch_rope((hipStream_t)stream, a), "rope launch");
+}

@@ -70,6 +70,18 @@ struct DequantRowsArgs {
   float *out;              // [rows][dim]
 };
 
+// Rotate-half RoPE of a fused projection [rows][heads + 2*kv_heads][dim]
+// (rows = B*T) into head-major q [B][heads][T][dim], k and v [B][kv_heads][T][dim].
+struct RopeArgs {
+  const uint16_t *qkv;
+  int64_t rows;
+  int tokens, heads, kv_heads, dim, float_kind;
+  const int32_t *positions;  // [rows]
+  const float *inv_freq;     // [dim/2]
+  uint16_t *q, *k, *v;
+};
+
+hipError_t launch_rope(hipStream_t stream, const RopeArgs &a);
 hipError_t launch_quantize_rows(hipStream_t stream, const QuantRowsArgs &a);
 hipError_t launch_dequantize_rows(hipStream_t stream, const DequantRowsArgs &a);
 hipError_t launch_append(hipStream_t stream, const AppendArgs &a);

@@ -47,6 +47,8 @@ SIGNATURES = {
                           ctypes.c_int),
     "pkv_dequantize_rows": ([_c_p, _c_p, _c_p, _c_p, _i64, _i32, _i32, _i32, _c_p],
                             ctypes.c_int),
+    "pkv_rope_qkv": ([_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p,
+                      _c_p], ctypes.c_int),
 }
 
 

@@ -111,13 +111,28 @@ class AttentionLayer:
             w = torch.randn((rows, cols), generator=gen, dtype=torch.float32) / math.sqrt(rows)
             return w.to(device=device, dtype=dtype)
 
-        self.wq, self.wk, self.wv = weight(h, hq * d), weight(h, hk * d), weight(h, hk * d)
+        wq, wk, wv = weight(h, hq * d), weight(h, hk * d), weight(h, hk * d)
+        # one fused q|k|v projection; wq/wk/wv are column views of it
+        self.wqkv = torch.cat([wq, wk, wv], dim=1)
+        self.wq = self.wqkv[:, :hq * d]
+        self.wk = self.wqkv[:, hq * d:(hq + hk) * d]
+        self.wv = self.wqkv[:, (hq + hk) * d:]
         self.wo = weight(hq * d, h)
         self.scale = 1.0 / math.sqrt(d)
         self.inv_freq = rope_inverse_frequencies(d, spec.rope_theta, spec.rope_scaling).to(device)
 
     def project(self, x, positions):
-        """``x [B, T, hidden]`` -> RoPE'd ``q [B, H, T, D]``, ``k, v [B, HK, T, D]``."""
+        """``x [B, T, hidden]`` -> RoPE'd ``q [B, H, T, D]``, ``k, v [B, HK, T, D]``:
+        one GEMM over the fused weight, then libpkv's RoPE kernel, which also
+        writes the head-major layouts (``transformer.py:146-184``)."""
+        from pkv import ops
+
+        s = self.spec
+        return ops.rope_qkv(x @ self.wqkv, positions, self.inv_freq, s.query_heads, s.kv_heads)
+
+    def project_reference(self, x, positions):
+        """The same projection as separate GEMMs and torch element-wise RoPE
+        (``apply_rope``): the comparison path of the tests."""
         s = self.spec
         batch, width, _ = x.shape
         q = (x @ self.wq).view(batch, width, s.query_heads, s.head_dim).transpose(1, 2)
@@ -130,8 +145,7 @@ class AttentionLayer:
         ``position_ids`` stay on the host for the cache's position check (no
         device sync); RoPE reads a device copy."""
         q, k, v = self.project(x, position_ids.to(x.device, non_blocking=True))
-        out = cache.attend(q.contiguous(), k.contiguous(), v.contiguous(), scale=self.scale,
-                           position_ids=position_ids)
+        out = cache.attend(q, k, v, scale=self.scale, position_ids=position_ids)
         batch, _, width, _ = out.shape
         return out.transpose(1, 2).reshape(batch, width, -1) @ self.wo
 

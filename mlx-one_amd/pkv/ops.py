@@ -246,3 +246,36 @@ def dequantize_rows(state, bits, dim, group_size=32):
                                           group_size, nat.ptr(out))
     nat.check(code, "dequantize")
     return out
+
+
+_FLOAT_KIND = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def rope_qkv(qkv, positions, inv_freq, heads, kv_heads):
+    """Rotate-half RoPE of a fused projection ``qkv [B, T, (heads + 2*kv_heads) * D]``
+    at ``positions [B, T]``: returns ``q [B, heads, T, D]``, ``k, v [B, kv_heads, T, D]``
+    (q and k rotated, v copied), contiguous, in ``qkv``'s dtype.  Float32 math as
+    the reference's ``apply_rope`` (``models/shared/transformer.py:32-90``)."""
+    if qkv.dim() != 3 or qkv.dtype not in _FLOAT_KIND or not qkv.is_cuda:
+        raise ValueError("qkv must be a [B, T, width] f16/bf16 device tensor")
+    batch, tokens, width = qkv.shape
+    if width % (heads + 2 * kv_heads):
+        raise ValueError("qkv width is not (heads + 2*kv_heads) * head_dim")
+    dim = width // (heads + 2 * kv_heads)
+    if dim % 2 or dim > 256 or inv_freq.numel() != dim // 2:
+        raise ValueError("RoPE needs an even head dimension <= 256 and dim/2 frequencies")
+    if tuple(positions.shape) != (batch, tokens):
+        raise ValueError("positions must be [B, T]")
+    device = qkv.device
+    qkv = qkv.contiguous()
+    pos = _i32(positions, device)
+    inv = inv_freq.to(device=device, dtype=torch.float32).contiguous()
+    q = torch.empty((batch, heads, tokens, dim), dtype=qkv.dtype, device=device)
+    k = torch.empty((batch, kv_heads, tokens, dim), dtype=qkv.dtype, device=device)
+    v = torch.empty_like(k)
+    code = nat.load().pkv_rope_qkv(nat.stream_handle(device), nat.ptr(qkv), batch, tokens, heads,
+                                   kv_heads, dim, _FLOAT_KIND[qkv.dtype], nat.ptr(pos),
+                                   nat.ptr(inv), nat.ptr(q), nat.ptr(k), nat.ptr(v))
+    nat.check(code, "rope")
+    return q, k, v
+

@@ -154,3 +154,25 @@ def test_status_codes_map_to_reference_exceptions():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(nat.NativeLibraryMissing):
         nat.load(tmp_path / "libpkv.so")
+
+
+@pytest.mark.parametrize("args", [
+    (1, 1, 8, 2, 127, 1),      # odd head dimension
+    (1, 1, 8, 2, 258, 1),      # head dimension above 256
+    (1, 1, 0, 2, 128, 1),      # no query heads
+    (1, 1, 8, 0, 128, 1),      # no KV heads
+    (1, 1, 8, 2, 128, 2),      # unknown float kind
+    (-1, 1, 8, 2, 128, 1),     # negative batch
+])
+def test_rope_rejects_bad_shapes(args):
+    lib = nat.load()
+    b, t, h, hk, d, kind = args
+    code = lib.pkv_rope_qkv(None, FAKE, b, t, h, hk, d, kind, FAKE, FAKE, FAKE, FAKE, FAKE)
+    assert code == nat.PKV_INVALID_ARGUMENT
+
+
+def test_rope_empty_batch_and_null_tensors():
+    lib = nat.load()
+    assert lib.pkv_rope_qkv(None, None, 0, 5, 8, 2, 128, 1, None, None, None, None, None) == nat.PKV_OK
+    assert lib.pkv_rope_qkv(None, None, 1, 1, 8, 2, 128, 1, FAKE, FAKE, FAKE, FAKE,
+                            FAKE) == nat.PKV_INVALID_ARGUMENT
