@@ -80,7 +80,10 @@ class BlockRef:
     def block(self) -> CacheBlock:
         if self.closed:
             raise CacheCorruptionError("block reference is closed")
-        return self.pool.get(self.block_id)
+        block = self.pool._blocks.get(self.block_id)   # one atomic dict read
+        if block is None:
+            raise CacheCorruptionError(f"unknown or freed KV block {self.block_id}")
+        return block
 
     def fork(self) -> "BlockRef":
         if self.closed:

@@ -73,27 +73,33 @@ class PagedRunner:
         self.last_trace = {}
 
     def _validate(self, requests):
+        """The reference's batch checks (``paged.py:308-345``), one pass per request."""
         if not requests:
             raise ValueError("empty paged batch")
         first = requests[0]
         layers = self.model.spec.layers
+        activation = self.model.activation_dtype
+        hidden = self.model.spec.hidden
+        pool_key = None
         for r in requests:
+            caches = r.cache
             if r.phase != first.phase or r.model_epoch != first.model_epoch \
-                    or len(r.cache) != len(first.cache):
+                    or len(caches) != len(first.cache):
                 raise ValueError("incompatible paged batch")
-            if (not r.cache or any(not isinstance(c, PagedKVCache) for c in r.cache)
-                    or len({c.offset for c in r.cache}) != 1
-                    or any(c.layer_id != i for i, c in enumerate(r.cache))
-                    or len(r.cache) != len(layers)):
+            if not caches or len(caches) != len(layers):
                 raise ValueError("invalid paged layer mappings")
+            offset = caches[0].offset if isinstance(caches[0], PagedKVCache) else None
+            for i, c in enumerate(caches):
+                if not isinstance(c, PagedKVCache) or c.offset != offset or c.layer_id != i:
+                    raise ValueError("invalid paged layer mappings")
             if r.handle is not None:
                 r.runtime._validate_handle(r.handle)
-                if r.handle.bundle.entries is not r.cache:
+                if r.handle.bundle.entries is not caches:
                     raise ValueError("paged request does not own its cache mapping")
-            if int(r.hidden.shape[0]) < 1 or int(r.hidden.shape[-1]) != self.model.spec.hidden:
+            if int(r.hidden.shape[0]) < 1 or int(r.hidden.shape[-1]) != hidden:
                 raise ValueError("request hidden states do not match the model")
-            for cache, layout in zip(r.cache, layers, strict=True):
-                if cache.dtype != self.model.activation_dtype:
+            for cache, layout in zip(caches, layers):
+                if cache.dtype != activation:
                     raise ModelCapabilityUnsupported("paged storage differs from execution precision")
                 # one layout per cache (append and adopt enforce it): its first page's
                 stored = cache.layout
@@ -101,10 +107,13 @@ class PagedRunner:
                                            or stored.head_dim != layout.key_dim
                                            or stored.layer_id != layout.layer_id):
                     raise ValueError("paged layer layout differs from the model")
-        if len({(id(c.pool), c.dtype, c.bits) for r in requests for c in r.cache}) != 1:
-            raise ValueError("incompatible paged pools or precision")
-        if any(r.runtime is not first.runtime for r in requests):
-            raise ValueError("paged batch spans cache managers")
+                key = (id(cache.pool), cache.dtype, cache.bits)
+                if pool_key is None:
+                    pool_key = key
+                elif key != pool_key:
+                    raise ValueError("incompatible paged pools or precision")
+            if r.runtime is not first.runtime:
+                raise ValueError("paged batch spans cache managers")
 
     def execute(self, requests):
         import torch
