@@ -143,7 +143,7 @@ class PagedRunner:
                 x[i, :widths[i]] = r.hidden
         # logical positions (padding columns continue the row), pinned so RoPE's
         # device copy does not stall the host
-        positions = torch.empty((len(requests), width), dtype=torch.int64,
+        positions = torch.empty((len(requests), width), dtype=torch.int32,
                                 pin_memory=device.type == "cuda")
         starts = np.array([r.cache[0].offset for r in requests], np.int64)
         positions.numpy()[:] = starts[:, None] + np.arange(width)[None, :]
