@@ -176,6 +176,11 @@ ATTN_CASES = {
                  "bfloat16", 40, 2),
     "f16_pages": (dict(name="c1", bits=16), "float16", 64, 1),
     "more_waves_than_tiles": (dict(name="c2", batch=2, lengths=(40, 3)), "bfloat16", 16, 10000),
+    # few waves per (sequence, KV head): one long sequence is cut into ~40
+    # pieces, the rest stay whole
+    "fused_skewed_many_pieces": (dict(name="c2", batch=8, heads=4, kv_heads=1,
+                                      lengths=(8000,) + (16,) * 7), "bfloat16", 256, 40),
+    "fused_gqa8_rows8": (dict(name="c3", batch=3, lengths=(900, 2048, 33)), "bfloat16", 128, 20),
     # wide query blocks (> 32 rows per KV head, or > 16 at head_dim 256) run
     # on the chunked-prefill kernel: 128-row blocks, causal over the chunk
     "prefill_c5_small": (dict(name="c5", batch=2, lengths=(300, 170), num_queries=128,
@@ -279,3 +284,49 @@ def test_prefill_ragged_widths(positions_given):
     want = oracle_attention(fmt, inst, positions, widths, scale)
     assert_attention_close(got, want)
     assert np.all(got[1, :, 17:] == 0) and np.all(got[2, :, 1:] == 0)
+
+
+def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays():
+    """Split segments merged by log-sum-exp in a fixed piece order: back-to-back
+    calls on one workspace, and replays of a captured graph (attention + merge
+    kernels, eager work between replays), each give the eager result bit for bit."""
+    from pkv import ops, workloads
+
+    w = workloads.get("c2", batch=6, length_range=(300, 2000))
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=128)
+    scale = scale_of(w.head_dim)
+    q = to_torch(inst.queries, fmt.dtype)
+    q_pos = torch.from_numpy(inst.positions).cuda()
+    waves = 3 * w.batch * w.kv_heads       # ~3 pieces per segment
+    first = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos, waves=waves)
+    second = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
+                                 waves=waves)
+    torch.cuda.synchronize()
+    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, 1, np.int32), scale)
+    assert_attention_close(first.float().cpu().numpy(), want)
+    assert torch.equal(first, second)
+
+    out = torch.empty_like(first)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos, waves=waves,
+                            out=out)                      # warm-up outside the capture
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
+                                waves=waves, out=out)
+    torch.cuda.current_stream().wait_stream(stream)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+        eager = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
+                                    waves=waves)       # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, first)
+
