@@ -184,6 +184,68 @@ int pkv_rope_qkv(void *stream, const void *qkv, int32_t batch, int32_t tokens, i
                  int32_t kv_heads, int32_t dim, int32_t float_kind, const int32_t *positions,
                  const float *inv_freq, void *q, void *k, void *v);
 
+/*
+ * Device-side page allocation.  Page ownership -- the free pages, a reference
+ * count per page, each sequence slot's page table and length -- lives in
+ * device memory, so a decode step needs no host bookkeeping and can be
+ * replayed as a graph.  Replaces the host BlockPool / SegmentedPageArena /
+ * PersistentPageTable bookkeeping and the clone tail copy
+ * (src/mlx_one/engine/block_cache.py:121-326, engine/arena.py:27-225,
+ * engine/paged.py:83-91); the reference has no device-side counterpart.
+ *
+ * state: pkv_arena_state_bytes(capacity) bytes, set up by pkv_arena_init:
+ *   int32 [0] free pages, [1] sticky error bits (PKV_ARENA_*), [16, 16+C) free
+ *   stack, [16+C, 16+2C) reference counts (C = capacity_pages).
+ * slot_table [num_slots][max_pages] int32 page ids (-1 = none; initialise to
+ * -1), slot_lens [num_slots] int32 tokens (initialise to 0).  One page id
+ * addresses the same page in every layer's pool.  The kernels run as one
+ * workgroup each; calls on one state must be ordered on one stream, and the
+ * slots of one call must be distinct.  Errors are reported in state[1]: a call
+ * that hits one leaves the affected slots unchanged.
+ */
+#define PKV_ARENA_OUT_OF_PAGES 1
+#define PKV_ARENA_TABLE_FULL 2
+#define PKV_ARENA_BAD_ARGUMENT 4
+#define PKV_ARENA_CORRUPT 8
+
+int64_t pkv_arena_state_bytes(int32_t capacity_pages);
+int pkv_arena_init(void *stream, void *state, int32_t capacity_pages);
+
+/*
+ * Grow slots[i] by widths[i] tokens: pages for the new tokens come off the free
+ * stack (reference count 1); a partly filled tail page shared with another slot
+ * is first copied, in each of the num_pools pools (page_bytes per page), to a
+ * page of its own (copy-on-write).  Writes the batch's operands for
+ * pkv_append_quantize / pkv_paged_attention: batch_table [count][max_pages]
+ * (the slot's pages, -1 past them), batch_starts [count] (length before),
+ * batch_lens [count] (length after).  If the free pages do not cover the call,
+ * no slot grows and PKV_ARENA_OUT_OF_PAGES is set.
+ */
+int pkv_arena_reserve(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                      int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                      const int32_t *slots, const int32_t *widths, int32_t count,
+                      void *const *pools, int32_t num_pools, int64_t page_bytes,
+                      int32_t *batch_table, int32_t *batch_starts, int32_t *batch_lens);
+
+/*
+ * Cut slots[i] back to keep_tokens[i] tokens (0 releases the slot): pages past
+ * the kept ones lose a reference and go back on the free stack at zero.  The
+ * transaction rollback of PagedKVCache (by length) and its release/trim
+ * (engine/paged.py:185-213).
+ */
+int pkv_arena_truncate(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                       int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                       const int32_t *slots, const int32_t *keep_tokens, int32_t count);
+
+/*
+ * dst_slots[i] (empty) becomes a copy of src_slots[i] sharing every page (one
+ * more reference each): PagedKVCache.clone / prefix adoption
+ * (engine/paged.py:77-101, :174-183), with the tail copied only when written.
+ */
+int pkv_arena_fork(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                   int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                   const int32_t *src_slots, const int32_t *dst_slots, int32_t count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -367,3 +367,101 @@ int pkv_rope_qkv(void *stream, const void *qkv, int32_t batch, int32_t tokens, i
   a.v = (uint16_t *)v;
   return check_launch(pkv::launch_rope((hipStream_t)stream, a), "rope launch");
 }
+
+// ---- device page allocator ------------------------------------------------------
+
+namespace {
+
+int arena_common(void *state, int32_t capacity_pages, int32_t page_tokens, int32_t *slot_table,
+                 int32_t num_slots, int32_t max_pages, int32_t *slot_lens, const int32_t *slots,
+                 const int32_t *arg, int32_t count, pkv::ArenaArgs *a) {
+  if (capacity_pages < 1 || capacity_pages > (1 << 30))
+    return fail(PKV_INVALID_ARGUMENT, "arena capacity must be 1..2^30 pages");
+  if (page_tokens != 16 && page_tokens != 32 && page_tokens != 64 && page_tokens != 128)
+    return fail(PKV_INVALID_ARGUMENT, "page_tokens must be 16, 32, 64 or 128");
+  if (num_slots < 1 || max_pages < 1 || (int64_t)max_pages * page_tokens > INT32_MAX)
+    return fail(PKV_INVALID_ARGUMENT, "invalid slot table shape");
+  if (count < 0) return fail(PKV_INVALID_ARGUMENT, "negative count");
+  if (!state || !slot_table || !slot_lens || (count > 0 && (!slots || !arg)))
+    return fail(PKV_INVALID_ARGUMENT, "NULL arena tensor");
+  a->state = (int32_t *)state;
+  a->capacity = capacity_pages;
+  a->page_tokens = page_tokens;
+  a->table = slot_table;
+  a->max_pages = max_pages;
+  a->num_slots = num_slots;
+  a->lens = slot_lens;
+  a->slots = slots;
+  a->arg = arg;
+  a->count = count;
+  a->num_pools = 0;
+  a->page_bytes = 0;
+  a->batch_table = a->batch_starts = a->batch_lens = nullptr;
+  return PKV_OK;
+}
+
+}  // namespace
+
+int64_t pkv_arena_state_bytes(int32_t capacity_pages) {
+  if (capacity_pages < 1 || capacity_pages > (1 << 30)) return -1;
+  return ((int64_t)pkv::kArenaHeaderWords + 2 * (int64_t)capacity_pages) * 4;
+}
+
+int pkv_arena_init(void *stream, void *state, int32_t capacity_pages) {
+  if (capacity_pages < 1 || capacity_pages > (1 << 30))
+    return fail(PKV_INVALID_ARGUMENT, "arena capacity must be 1..2^30 pages");
+  if (!state) return fail(PKV_INVALID_ARGUMENT, "NULL arena state");
+  return check_launch(pkv::launch_arena_init((hipStream_t)stream, (int32_t *)state, capacity_pages),
+                      "arena init launch");
+}
+
+int pkv_arena_reserve(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                      int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                      const int32_t *slots, const int32_t *widths, int32_t count,
+                      void *const *pools, int32_t num_pools, int64_t page_bytes,
+                      int32_t *batch_table, int32_t *batch_starts, int32_t *batch_lens) {
+  pkv::ArenaArgs a;
+  if (int rc = arena_common(state, capacity_pages, page_tokens, slot_table, num_slots, max_pages,
+                            slot_lens, slots, widths, count, &a))
+    return rc;
+  if (num_pools < 0 || num_pools > pkv::kMaxArenaPools)
+    return fail(PKV_INVALID_ARGUMENT, "arena pools must number 0..128");
+  if (num_pools > 0 && (!pools || page_bytes < 16 || page_bytes % 16))
+    return fail(PKV_INVALID_ARGUMENT, "arena pools need pointers and a page size that is a multiple of 16");
+  for (int l = 0; l < num_pools; ++l) {
+    if (!pools[l]) return fail(PKV_INVALID_ARGUMENT, "NULL arena pool");
+    a.pools[l] = (uint8_t *)pools[l];
+  }
+  if (count > 0 && (!batch_table || !batch_starts || !batch_lens))
+    return fail(PKV_INVALID_ARGUMENT, "reserve needs the batch table, starts and lengths outputs");
+  a.num_pools = num_pools;
+  a.page_bytes = page_bytes;
+  a.batch_table = batch_table;
+  a.batch_starts = batch_starts;
+  a.batch_lens = batch_lens;
+  return check_launch(pkv::launch_arena((hipStream_t)stream, pkv::ArenaOp::Reserve, a),
+                      "arena reserve launch");
+}
+
+int pkv_arena_truncate(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                       int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                       const int32_t *slots, const int32_t *keep_tokens, int32_t count) {
+  pkv::ArenaArgs a;
+  if (int rc = arena_common(state, capacity_pages, page_tokens, slot_table, num_slots, max_pages,
+                            slot_lens, slots, keep_tokens, count, &a))
+    return rc;
+  return check_launch(pkv::launch_arena((hipStream_t)stream, pkv::ArenaOp::Release, a),
+                      "arena truncate launch");
+}
+
+int pkv_arena_fork(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
+                   int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,
+                   const int32_t *src_slots, const int32_t *dst_slots, int32_t count) {
+  pkv::ArenaArgs a;
+  if (int rc = arena_common(state, capacity_pages, page_tokens, slot_table, num_slots, max_pages,
+                            slot_lens, src_slots, dst_slots, count, &a))
+    return rc;
+  return check_launch(pkv::launch_arena((hipStream_t)stream, pkv::ArenaOp::Fork, a),
+                      "arena fork launch");
+}
+

@@ -1,0 +1,323 @@
+// pkv_arena.hip -- device-side page allocation for the paged cache.
+//
+// The reference keeps page ownership on the host: BlockPool refcounts, pins
+// and seals (src/mlx_one/engine/block_cache.py:121-326), the arena's segment
+// staging (engine/arena.py:90-113) and a page table per layer cache
+// (arena.py:172-225), with a copy of the mutable tail page for every clone
+// (engine/paged.py:83-91).  Here the same ownership lives in device memory so a
+// decode step needs no host bookkeeping and can be replayed as a graph:
+//
+//   state  [0] free pages (the stack's height)  [1] sticky error bits
+//          [16, 16 + C)      free stack of page ids (C = capacity)
+//          [16 + C, 16 + 2C) reference count per page
+//   table  [slots][max_pages] page ids of each sequence slot, -1 past its end
+//   lens   [slots]            tokens of each slot
+//
+// One page id addresses the same page in every layer's pool (all layers of a
+// sequence grow together), so one reservation serves a whole model step.
+// Pages are shared by reference count (fork); the first append into a shared,
+// partly filled tail page copies it first (copy-on-write), which gives the
+// reference's clone semantics without copying tails that are never written.
+//
+// Every kernel runs as one workgroup: its reads and writes of the stack height
+// need no atomics, and it sees a consistent state whatever came before it on
+// the stream.  Calls on one state must be ordered (one stream).
+
+#include "pkv_device.h"
+#include "pkv_launch.h"
+
+namespace pkv {
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Inclusive prefix sum over the workgroup; *total receives the sum.
+__device__ __forceinline__ int block_scan_incl(int v, int *s_wave, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int incl = wave_scan_incl(v, lane);
+  if (lane == 63) s_wave[wave] = incl;
+  __syncthreads();
+  int before = 0, sum = 0;
+  for (int k = 0; k < kWaves; ++k) {
+    const int t = s_wave[k];
+    before += k < wave ? t : 0;
+    sum += t;
+  }
+  __syncthreads();  // s_wave is reused by the next scan
+  *total = sum;
+  return incl + before;
+}
+
+struct ArenaRefs {
+  int32_t *top, *err, *stack, *ref;
+  __device__ ArenaRefs(const ArenaArgs &a)
+      : top(a.state), err(a.state + 1), stack(a.state + kArenaHeaderWords),
+        ref(a.state + kArenaHeaderWords + a.capacity) {}
+};
+
+__global__ void arena_init_kernel(int32_t *state, int capacity) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < kArenaHeaderWords) state[i] = i == 0 ? capacity : 0;
+  if (i < capacity) {
+    state[kArenaHeaderWords + i] = capacity - 1 - (int)i;  // pops hand out 0, 1, 2, ...
+    state[kArenaHeaderWords + capacity + i] = 0;
+  }
+}
+
+// Reserve pages for `count` slots growing by arg[i] tokens each (slots distinct).
+// A slot that cannot grow (its table is full, or the stack is short -- then no
+// slot of the chunk grows) keeps its length, and its batch row ends before the
+// page its first new token would go to, so an append writes nothing.
+__global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
+  __shared__ int s_wave[kWaves];
+  __shared__ int s_top, s_fail, s_ncow;
+  __shared__ int s_slot[kThreads], s_keep[kThreads];
+  __shared__ int s_cow_src[kThreads], s_cow_dst[kThreads];
+  const ArenaRefs r(a);
+  const int P = a.page_tokens, mp = a.max_pages;
+  for (int c0 = 0; c0 < a.count; c0 += kThreads) {
+    const int i = c0 + threadIdx.x;
+    int s = -1, w = 0, L = 0, nl = 0, oldp = 0, newp = 0, need = 0, tail = -1;
+    bool cow = false, blocked = false;
+    if (i < a.count) {
+      s = a.slots[i];
+      w = a.arg[i];
+      if (s < 0 || s >= a.num_slots || w < 0) {
+        atomicOr(r.err, kArenaBadArgument);
+        s = -1;
+      } else {
+        L = a.lens[s];
+        nl = L + w;
+        oldp = cdiv(L, P);
+        if ((int64_t)nl > (int64_t)mp * P) {
+          atomicOr(r.err, kArenaTableFull);
+          blocked = true;
+        } else if (w > 0 && L % P != 0) {
+          tail = a.table[(int64_t)s * mp + L / P];
+          if (tail < 0 || tail >= a.capacity) {
+            atomicOr(r.err, kArenaCorrupt);
+            blocked = true;
+          } else if (atomicSub(&r.ref[tail], 1) > 1) {
+            cow = true;  // shared with another slot: write into a copy
+          } else {
+            atomicAdd(&r.ref[tail], 1);  // this slot holds the only reference
+          }
+        }
+        if (blocked) nl = L;
+        newp = cdiv(nl, P);
+        need = newp - oldp + (cow ? 1 : 0);
+      }
+    }
+    int total;
+    const int incl = block_scan_incl(need, s_wave, &total);
+    if (threadIdx.x == 0) {
+      s_top = *r.top;
+      s_fail = s_top < total;
+      if (s_fail) atomicOr(r.err, kArenaOutOfPages);
+      else *r.top = s_top - total;
+      s_ncow = 0;
+    }
+    __syncthreads();
+    if (s >= 0 && s_fail && w > 0) {
+      if (cow) atomicAdd(&r.ref[tail], 1);  // nothing taken: give the reference back
+      blocked = true;
+      nl = L;
+    }
+    if (s >= 0 && !s_fail && !blocked) {
+      int pos = s_top - 1 - (incl - need);  // this slot's pages: stack[pos], stack[pos - 1], ...
+      if (cow) {
+        const int np = r.stack[pos--];
+        if (np >= 0 && np < a.capacity) {
+          a.table[(int64_t)s * mp + L / P] = np;
+          r.ref[np] = 1;
+          const int k = atomicAdd(&s_ncow, 1);
+          s_cow_src[k] = tail;
+          s_cow_dst[k] = np;
+        } else {
+          atomicOr(r.err, kArenaCorrupt);
+        }
+      }
+      for (int p = oldp; p < newp; ++p) {
+        const int np = r.stack[pos--];
+        if (np >= 0 && np < a.capacity) {
+          a.table[(int64_t)s * mp + p] = np;
+          r.ref[np] = 1;
+        } else {
+          a.table[(int64_t)s * mp + p] = -1;
+          atomicOr(r.err, kArenaCorrupt);
+        }
+      }
+      a.lens[s] = nl;
+    }
+    if (i < a.count) {
+      a.batch_starts[i] = L;
+      a.batch_lens[i] = nl;
+    }
+    s_slot[threadIdx.x] = s;
+    s_keep[threadIdx.x] = blocked ? L / P : cdiv(nl, P);
+    __syncthreads();
+    // copy-on-write: the shared tail's bytes into the new page, in every layer's pool
+    const int64_t vecs = a.page_bytes / 16;
+    for (int k = 0; k < s_ncow; ++k)
+      for (int l = 0; l < a.num_pools; ++l) {
+        const u4 *src = (const u4 *)(a.pools[l] + (int64_t)s_cow_src[k] * a.page_bytes);
+        u4 *dst = (u4 *)(a.pools[l] + (int64_t)s_cow_dst[k] * a.page_bytes);
+        for (int64_t v = threadIdx.x; v < vecs; v += kThreads) dst[v] = src[v];
+      }
+    // the batch's block-table rows: the slot's pages, -1 past them
+    const int rows = min(kThreads, a.count - c0);
+    for (int64_t e = threadIdx.x; e < (int64_t)rows * mp; e += kThreads) {
+      const int row = (int)(e / mp), p = (int)(e - (int64_t)row * mp);
+      const int sl = s_slot[row];
+      a.batch_table[(int64_t)(c0 + row) * mp + p] =
+          sl >= 0 && p < s_keep[row] ? a.table[(int64_t)sl * mp + p] : -1;
+    }
+    __syncthreads();  // LDS reuse by the next chunk
+  }
+}
+
+// Per-item page ranges [from, to) of `count` items, flattened over the
+// workgroup: calls f(item, page index) for every page of every item.
+template <typename F>
+__device__ __forceinline__ void for_each_page(const int *s_from, const int *s_to, int n, int *s_wave,
+                                              int *s_base, F f) {
+  const int t = threadIdx.x;
+  const int len = t < n ? s_to[t] - s_from[t] : 0;
+  int total;
+  const int incl = block_scan_incl(len, s_wave, &total);
+  s_base[t] = incl - len;
+  __syncthreads();
+  for (int e = t; e < total; e += kThreads) {
+    int lo = 0, hi = n - 1;  // the last item whose base <= e
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_base[mid] <= e) lo = mid; else hi = mid - 1;
+    }
+    f(lo, s_from[lo] + (e - s_base[lo]));
+  }
+  __syncthreads();
+}
+
+// Truncate slots to arg[i] tokens (0 releases the slot's pages); pages whose
+// last reference goes back on the free stack.
+__global__ __launch_bounds__(kThreads) void arena_release_kernel(ArenaArgs a) {
+  __shared__ int s_wave[kWaves];
+  __shared__ int s_slot[kThreads], s_from[kThreads], s_to[kThreads], s_base[kThreads];
+  __shared__ int s_top, s_freed;
+  const ArenaRefs r(a);
+  const int P = a.page_tokens, mp = a.max_pages;
+  if (threadIdx.x == 0) { s_top = *r.top; s_freed = 0; }
+  for (int c0 = 0; c0 < a.count; c0 += kThreads) {
+    const int i = c0 + threadIdx.x;
+    int s = -1, from = 0, to = 0;
+    if (i < a.count) {
+      s = a.slots[i];
+      const int keep = a.arg[i];
+      if (s < 0 || s >= a.num_slots) {
+        atomicOr(r.err, kArenaBadArgument);
+        s = -1;
+      } else {
+        const int L = a.lens[s];
+        if (keep < 0 || keep > L) {
+          atomicOr(r.err, kArenaBadArgument);
+          s = -1;
+        } else {
+          from = cdiv(keep, P);
+          to = cdiv(L, P);
+          a.lens[s] = keep;
+        }
+      }
+    }
+    s_slot[threadIdx.x] = s;
+    s_from[threadIdx.x] = s >= 0 ? from : 0;
+    s_to[threadIdx.x] = s >= 0 ? to : 0;
+    __syncthreads();
+    const int n = min(kThreads, a.count - c0);
+    for_each_page(s_from, s_to, n, s_wave, s_base, [&](int item, int p) {
+      int32_t *entry = a.table + (int64_t)s_slot[item] * mp + p;
+      const int id = *entry;
+      *entry = -1;
+      if (id < 0 || id >= a.capacity) {
+        atomicOr(r.err, kArenaCorrupt);
+        return;
+      }
+      const int before = atomicSub(&r.ref[id], 1);
+      if (before == 1) {
+        const int k = atomicAdd(&s_freed, 1);
+        if (s_top + k < a.capacity) r.stack[s_top + k] = id;
+        else atomicOr(r.err, kArenaCorrupt);
+      } else if (before < 1) {
+        atomicOr(r.err, kArenaCorrupt);
+      }
+    });
+  }
+  if (threadIdx.x == 0) *r.top = min(s_top + s_freed, a.capacity);
+}
+
+// Fork: slot arg[i] (empty) becomes a copy of slot slots[i] sharing its pages.
+__global__ __launch_bounds__(kThreads) void arena_fork_kernel(ArenaArgs a) {
+  __shared__ int s_wave[kWaves];
+  __shared__ int s_src[kThreads], s_dst[kThreads], s_from[kThreads], s_to[kThreads], s_base[kThreads];
+  const ArenaRefs r(a);
+  const int P = a.page_tokens, mp = a.max_pages;
+  for (int c0 = 0; c0 < a.count; c0 += kThreads) {
+    const int i = c0 + threadIdx.x;
+    int src = -1, dst = -1, n = 0;
+    if (i < a.count) {
+      src = a.slots[i];
+      dst = a.arg[i];
+      if (src < 0 || src >= a.num_slots || dst < 0 || dst >= a.num_slots || src == dst ||
+          a.lens[dst] != 0) {
+        atomicOr(r.err, kArenaBadArgument);
+        src = dst = -1;
+      } else {
+        n = cdiv(a.lens[src], P);
+      }
+    }
+    s_src[threadIdx.x] = src;
+    s_dst[threadIdx.x] = dst;
+    s_from[threadIdx.x] = 0;
+    s_to[threadIdx.x] = n;
+    __syncthreads();
+    const int items = min(kThreads, a.count - c0);
+    for_each_page(s_from, s_to, items, s_wave, s_base, [&](int item, int p) {
+      const int id = a.table[(int64_t)s_src[item] * mp + p];
+      a.table[(int64_t)s_dst[item] * mp + p] = id;
+      if (id >= 0 && id < a.capacity) atomicAdd(&r.ref[id], 1);
+      else atomicOr(r.err, kArenaCorrupt);
+    });
+    if (dst >= 0) a.lens[dst] = a.lens[src];
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+hipError_t launch_arena_init(hipStream_t stream, int32_t *state, int capacity) {
+  const int64_t n = capacity > kArenaHeaderWords ? capacity : kArenaHeaderWords;
+  hipLaunchKernelGGL(arena_init_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, state,
+                     capacity);
+  return hipGetLastError();
+}
+
+hipError_t launch_arena(hipStream_t stream, ArenaOp op, const ArenaArgs &a) {
+  if (a.count <= 0) return hipSuccess;
+  switch (op) {
+    case ArenaOp::Reserve:
+      hipLaunchKernelGGL(arena_reserve_kernel, dim3(1), dim3(kThreads), 0, stream, a);
+      break;
+    case ArenaOp::Release:
+      hipLaunchKernelGGL(arena_release_kernel, dim3(1), dim3(kThreads), 0, stream, a);
+      break;
+    case ArenaOp::Fork:
+      hipLaunchKernelGGL(arena_fork_kernel, dim3(1), dim3(kThreads), 0, stream, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pkv

@@ -82,6 +82,32 @@ struct RopeArgs {
 };
 
 hipError_t launch_rope(hipStream_t stream, const RopeArgs &a);
+
+// Device page allocator (pkv_arena.hip).  State words: [0] free pages,
+// [1] error bits, header padded to kArenaHeaderWords, then the free stack
+// [capacity] and the reference counts [capacity].
+constexpr int kArenaHeaderWords = 16;
+constexpr int kMaxArenaPools = 128;
+constexpr int kArenaOutOfPages = 1, kArenaTableFull = 2, kArenaBadArgument = 4, kArenaCorrupt = 8;
+
+enum class ArenaOp { Reserve, Release, Fork };
+
+struct ArenaArgs {
+  int32_t *state;
+  int capacity, page_tokens;
+  int32_t *table;   // [num_slots][max_pages]
+  int max_pages, num_slots;
+  int32_t *lens;    // [num_slots]
+  const int32_t *slots, *arg;  // per item: slot, and width / kept tokens / fork destination
+  int count;
+  uint8_t *pools[kMaxArenaPools];  // reserve: copy-on-write in every layer's pool
+  int num_pools;
+  int64_t page_bytes;
+  int32_t *batch_table, *batch_starts, *batch_lens;  // reserve outputs
+};
+
+hipError_t launch_arena_init(hipStream_t stream, int32_t *state, int capacity);
+hipError_t launch_arena(hipStream_t stream, ArenaOp op, const ArenaArgs &a);
 hipError_t launch_quantize_rows(hipStream_t stream, const QuantRowsArgs &a);
 hipError_t launch_dequantize_rows(hipStream_t stream, const DequantRowsArgs &a);
 hipError_t launch_append(hipStream_t stream, const AppendArgs &a);

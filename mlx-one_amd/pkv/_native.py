@@ -49,6 +49,14 @@ SIGNATURES = {
                             ctypes.c_int),
     "pkv_rope_qkv": ([_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p,
                       _c_p], ctypes.c_int),
+    "pkv_arena_state_bytes": ([_i32], _i64),
+    "pkv_arena_init": ([_c_p, _c_p, _i32], ctypes.c_int),
+    "pkv_arena_reserve": ([_c_p, _c_p, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32,
+                           _c_p, _i32, _i64, _c_p, _c_p, _c_p], ctypes.c_int),
+    "pkv_arena_truncate": ([_c_p, _c_p, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32],
+                           ctypes.c_int),
+    "pkv_arena_fork": ([_c_p, _c_p, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32],
+                       ctypes.c_int),
 }
 
 

@@ -176,3 +176,32 @@ def test_rope_empty_batch_and_null_tensors():
     assert lib.pkv_rope_qkv(None, None, 0, 5, 8, 2, 128, 1, None, None, None, None, None) == nat.PKV_OK
     assert lib.pkv_rope_qkv(None, None, 1, 1, 8, 2, 128, 1, FAKE, FAKE, FAKE, FAKE,
                             FAKE) == nat.PKV_INVALID_ARGUMENT
+
+
+def test_arena_state_size_and_argument_checks():
+    lib = nat.load()
+    assert lib.pkv_arena_state_bytes(100) == (16 + 200) * 4
+    assert lib.pkv_arena_state_bytes(0) < 0
+    assert lib.pkv_arena_init(None, None, 10) == nat.PKV_INVALID_ARGUMENT
+    assert lib.pkv_arena_init(None, FAKE, 0) == nat.PKV_INVALID_ARGUMENT
+    common = (None, FAKE, 64, 16, FAKE, 8, 32, FAKE)
+    pools = (ctypes.c_void_p * 1)(4096)
+    # nothing to do: returns before any HIP call
+    assert lib.pkv_arena_reserve(*common, None, None, 0, None, 0, 0, None, None, None) == nat.PKV_OK
+    assert lib.pkv_arena_truncate(*common, None, None, 0) == nat.PKV_OK
+    assert lib.pkv_arena_fork(*common, None, None, 0) == nat.PKV_OK
+    bad = [
+        (None, FAKE, 64, 24, FAKE, 8, 32, FAKE),   # page_tokens
+        (None, FAKE, 0, 16, FAKE, 8, 32, FAKE),    # capacity
+        (None, FAKE, 64, 16, FAKE, 0, 32, FAKE),   # slots
+        (None, None, 64, 16, FAKE, 8, 32, FAKE),   # state
+    ]
+    for args in bad:
+        assert lib.pkv_arena_truncate(*args, FAKE, FAKE, 1) == nat.PKV_INVALID_ARGUMENT
+    assert lib.pkv_arena_truncate(*common, FAKE, FAKE, -1) == nat.PKV_INVALID_ARGUMENT
+    assert lib.pkv_arena_reserve(*common, FAKE, FAKE, 1, pools, 200, 4096, FAKE, FAKE,
+                                 FAKE) == nat.PKV_INVALID_ARGUMENT      # pools
+    assert lib.pkv_arena_reserve(*common, FAKE, FAKE, 1, pools, 1, 10, FAKE, FAKE,
+                                 FAKE) == nat.PKV_INVALID_ARGUMENT      # page bytes
+    assert lib.pkv_arena_reserve(*common, FAKE, FAKE, 1, pools, 1, 4096, None, FAKE,
+                                 FAKE) == nat.PKV_INVALID_ARGUMENT      # outputs
