@@ -316,6 +316,88 @@ def layer_bench(args):
     return 0
 
 
+def layer_device_bench(args):
+    """The same layer decode steps with the page bookkeeping on the device
+    (``DevicePageArena`` + ``DeviceRunner``): one reservation kernel per step
+    instead of per-sequence host page tables.  With ``--graph`` each timed step
+    is one replay of a captured decode step (reserve, QKV GEMM, RoPE, append,
+    attention, merge, output GEMM); otherwise an eager ``DeviceRunner.execute``."""
+    import numpy as np
+    import torch
+
+    from pkv import _native, workloads
+    from pkv.device_arena import DevicePageArena, DeviceRunner
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.ops import PageFormat
+
+    _native.load()
+    device = torch.device("cuda:0")
+    w = workloads.get("c2")
+    inst = workloads.generate(w, kv=False)
+    spec = ModelSpec(hidden=4096, query_heads=w.heads, kv_heads=w.kv_heads, head_dim=w.head_dim,
+                     num_layers=1, dtype="float16")
+    model = AttentionStack(spec, device=device, seed=w.seed)
+    fmt = PageFormat(w.kv_heads, w.head_dim, w.page_tokens, 8, w.group_size, torch.float16)
+    context = [int(x) for x in inst.context]
+    extra = args.warmup + args.steps + 2
+    longest = max(context) + extra
+    pages = sum(-(-(c + extra) // w.page_tokens) for c in context) + w.batch
+    arena = DevicePageArena(fmt, pages, num_layers=1, max_slots=w.batch, max_tokens=longest,
+                            device=device)
+    runner = DeviceRunner(model, arena)
+    slots = [arena.open_slot() for _ in range(w.batch)]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    chunk = 1024
+    while True:
+        left = [c - arena.lengths[s] for c, s in zip(context, slots)]
+        rows = [b for b in range(w.batch) if left[b] > 0]
+        if not rows:
+            break
+        widths = [min(chunk, left[b]) for b in rows]
+        hidden = torch.randn((len(rows), max(widths), spec.hidden), generator=gen, device=device,
+                             dtype=torch.float16)
+        runner.execute([slots[b] for b in rows], hidden, widths)
+    arena.check()
+    decode_in = torch.randn((args.warmup + args.steps, w.batch, 1, spec.hidden), generator=gen,
+                            device=device, dtype=torch.float16)
+    if args.graph:
+        x = decode_in[0].clone()
+        captured = runner.capture_decode(slots, x)      # runs one step eagerly
+        replay = captured.replay
+
+        def step(i):
+            x.copy_(decode_in[i])
+            replay()
+    else:
+        def step(i):
+            runner.execute(slots, decode_in[i])
+    for i in range(1, args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    arena.sync_lengths()
+    arena.check()
+    result = {
+        "metric": "e2e attention-layer decode tok/s (device page arena, Llama-3-8B layer, q8_0 KV)",
+        "value": round(w.batch / (ms / 1e3), 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "layer", "arena": "device", "graph": bool(args.graph),
+                   "batch": w.batch, "hidden": spec.hidden, "heads": spec.query_heads,
+                   "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "kv": "q8_0",
+                   "group_size": w.group_size, "page_tokens": w.page_tokens,
+                   "mean_context": float(np.mean([arena.lengths[s] for s in slots]))},
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -330,6 +412,9 @@ def main(argv=None):
                         help="replay the timed steps as one captured HIP graph")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
                         help="seconds of CPU baseline timing (0 disables)")
+    parser.add_argument("--arena", choices=("host", "device"), default="host",
+                        help="layer workload: page bookkeeping on the host (PagedRunner) or "
+                             "the device (DeviceRunner)")
     parser.add_argument("--copy-probe", action="store_true",
                         help="only run three 256 MiB device copies (calibrates rocprofv3 "
                              "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic)")
@@ -340,7 +425,7 @@ def main(argv=None):
         if args.gpus != 1:
             print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
             return 2
-        return layer_bench(args)
+        return layer_device_bench(args) if args.arena == "device" else layer_bench(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the paged decode path "
                           "shards by sequence with no exchange; run with --gpus 1"}))

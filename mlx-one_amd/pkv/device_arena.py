@@ -180,6 +180,10 @@ class DevicePageArena:
                 self.lengths[d] = self.lengths[s]
 
     # -- inspection (these synchronise) ---------------------------------------------------
+    def sync_lengths(self):
+        """Refresh the host length mirror from the device (after graph replays)."""
+        self.lengths = [int(x) for x in self.lens.cpu().tolist()]
+
     def status(self):
         """``(free_pages, error_bits)``."""
         head = self.state[:2].cpu().tolist()
@@ -228,3 +232,78 @@ class DeviceBatchCache:
         out = ops.paged_attention(fmt, pool, queries.to(dtype).contiguous(), self.res.table,
                                   self.res.lens, scale=scale, widths=self.res.widths)
         return out.to(queries.dtype)
+
+
+class DeviceRunner:
+    """Batch steps of a model over device-arena slots: ``PagedRunner.execute``
+    (``engine/paged.py:308-417``) with the page bookkeeping on the device.  One
+    reservation covers every layer; a step that raises is rolled back by
+    length (``truncate`` to the lengths before it)."""
+
+    def __init__(self, model, arena):
+        if len(arena.pools) != model.spec.num_layers:
+            raise ValueError("the arena needs one pool per model layer")
+        self.model, self.arena = model, arena
+
+    def _forward(self, hidden, res):
+        batch, width, _ = hidden.shape
+        positions = res.starts.view(batch, 1)
+        if width > 1:
+            positions = positions + torch.arange(width, dtype=torch.int32, device=hidden.device)
+        caches = tuple(DeviceBatchCache(self.arena, layer, res)
+                       for layer in range(len(self.arena.pools)))
+        return self.model.forward(hidden, cache=caches, position_ids=positions)
+
+    def execute(self, slots, hidden, widths=None):
+        """``hidden [B, T, hidden]`` for ``slots`` (row b's columns past
+        ``widths[b]`` are padding); returns the model's ``[B, T, hidden]``."""
+        batch, width, _ = hidden.shape
+        slots = [int(s) for s in slots]
+        widths = [width] * batch if widths is None else [int(w) for w in widths]
+        if len(slots) != batch or len(widths) != batch or any(w < 1 or w > width for w in widths):
+            raise ValueError("one slot and a width in 1..T per row")
+        before = [self.arena.lengths[s] for s in slots]
+        res = self.arena.reserve(slots, widths)
+        try:
+            return self._forward(hidden, res)
+        except BaseException:
+            self.arena.truncate(slots, before)
+            raise
+
+    def capture_decode(self, slots, hidden):
+        """A graph of one decode step (one token per slot) reading the static
+        buffer ``hidden [B, 1, hidden]``: returns a ``CapturedStep`` whose
+        ``replay()`` appends a token to every slot and leaves the step's output
+        in ``out``.  Runs one step eagerly first (it sizes the buffers and
+        warms the libraries).  Replays do not advance the host length mirror:
+        ``arena.sync_lengths()`` reads the device's."""
+        slots_d = torch.tensor([int(s) for s in slots], dtype=torch.int32, device=self.arena.device)
+        widths_d = torch.ones_like(slots_d)
+        res = self.arena.reserve(slots_d, widths_d)
+        self._forward(hidden, res)
+        torch.cuda.synchronize(self.arena.device)
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(self.arena.device)
+        stream.wait_stream(torch.cuda.current_stream(self.arena.device))
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                res_g = self.arena.reserve(slots_d, widths_d, out=res)
+                out = self._forward(hidden, res_g)
+        torch.cuda.current_stream(self.arena.device).wait_stream(stream)
+        self.arena.sync_lengths()
+        return CapturedStep(graph, out, hidden, res, (slots_d, widths_d))
+
+
+@dataclass
+class CapturedStep:
+    """A captured decode step and every buffer from outside the capture that its
+    kernels read or write: they must live as long as the graph."""
+
+    graph: torch.cuda.CUDAGraph
+    out: torch.Tensor               # the step's output, rewritten by each replay
+    hidden: torch.Tensor            # the static input buffer
+    reservation: Reservation        # the batch operands the reserve kernel rewrites
+    operands: tuple                 # slot ids and widths read by the reserve kernel
+
+    def replay(self):
+        self.graph.replay()

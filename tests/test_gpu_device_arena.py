@@ -271,3 +271,77 @@ def test_graph_replays_of_a_decode_step_equal_eager_steps():
     assert arena.lens[slots].tolist() == [37 + 4, 16 + 4, 5 + 4, 90 + 4]
     arena.lengths = [int(x) for x in arena.lens.cpu()]
     _invariants(arena)
+
+
+def test_device_runner_matches_the_host_runner_and_rolls_back():
+    """The same layer steps through PagedRunner (host pages) and DeviceRunner
+    (device pages) give the same outputs bit for bit; a step that raises leaves
+    the device slots at their lengths before it; captured decode steps equal
+    eager ones."""
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.device_arena import DevicePageArena, DeviceRunner
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.ops import PageFormat
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, device="cuda", seed=5)
+    cm = CacheManager(model, CacheConfig(block_size_tokens=16, key_type="q8_0", value_type="q8_0",
+                                         group_size=32, memory_budget_bytes=1 << 30))
+    handles = [cm.create_handle(f"r{b}", key_type="q8_0", value_type="q8_0") for b in range(3)]
+    host = PagedRunner(model)
+    arena = DevicePageArena(PageFormat(2, 64, 16, 8, 32, torch.float16), 64, num_layers=2,
+                            max_slots=4, max_tokens=256)
+    dev = DeviceRunner(model, arena)
+    slots = [arena.open_slot() for _ in range(3)]
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    for widths in ([40, 17, 3], [1, 1, 1], [5, 1, 9], [1, 1, 1]):
+        width = max(widths)
+        x = torch.randn((3, width, 256), generator=gen, device="cuda").half()
+        for b, n in enumerate(widths):
+            x[b, n:] = 0
+        got = dev.execute(slots, x, widths)
+        phase = "prefill" if width > 1 else "decode"
+        out = host.execute([ForwardRequest(h.request_id, x[b, :n], h.bundle.entries, phase=phase,
+                                           runtime=cm, handle=h, return_all_logits=True)
+                            for b, (h, n) in enumerate(zip(handles, widths))])
+        torch.cuda.synchronize()
+        for b, n in enumerate(widths):
+            assert torch.equal(got[b, :n], out.logits[b][0]), (widths, b)
+    arena.check()
+    assert arena.lengths[:3] == [h.token_count for h in handles]
+
+    before = list(arena.lengths)
+
+    class Boom(RuntimeError):
+        pass
+
+    def broken(*_a, **_k):
+        raise Boom
+
+    forward = model.forward
+    model.forward = broken
+    with pytest.raises(Boom):
+        dev.execute(slots, torch.zeros((3, 1, 256), device="cuda").half())
+    model.forward = forward
+    arena.sync_lengths()
+    assert arena.lengths == before
+    _invariants(arena)
+
+    x = torch.randn((3, 1, 256), generator=gen, device="cuda").half()
+    step = dev.capture_decode(slots, x)                # one eager step, then the graph
+    out = step.out
+    host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm, handle=h)
+                  for b, h in enumerate(handles)])     # the host runner takes the same step
+    for i in range(3):
+        x.copy_(torch.randn((3, 1, 256), generator=gen, device="cuda").half())
+        step.replay()
+        ref = host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm,
+                                           handle=h) for b, h in enumerate(handles)])
+        torch.cuda.synchronize()
+        for b in range(3):
+            assert torch.equal(out[b, 0], ref.logits[b][0, 0]), (i, b)
+    arena.sync_lengths()
+    assert arena.lengths[:3] == [h.token_count for h in handles]
+    _invariants(arena)
