@@ -217,9 +217,12 @@ int pkv_arena_init(void *stream, void *state, int32_t capacity_pages);
  * is first copied, in each of the num_pools pools (page_bytes per page), to a
  * page of its own (copy-on-write).  Writes the batch's operands for
  * pkv_append_quantize / pkv_paged_attention: batch_table [count][max_pages]
- * (the slot's pages, -1 past them), batch_starts [count] (length before),
+ * (the slot's pages; entries past them are not written -- those kernels read
+ * a row only up to its length), batch_starts [count] (length before),
  * batch_lens [count] (length after).  If the free pages do not cover the call,
- * no slot grows and PKV_ARENA_OUT_OF_PAGES is set.
+ * no slot grows, PKV_ARENA_OUT_OF_PAGES is set, and each growing slot's batch
+ * row holds -1 from the page its first new token would go to (an append then
+ * writes nothing).
  */
 int pkv_arena_reserve(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
                       int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,

@@ -69,19 +69,26 @@ __global__ void arena_init_kernel(int32_t *state, int capacity) {
 }
 
 // Reserve pages for `count` slots growing by arg[i] tokens each (slots distinct).
-// A slot that cannot grow (its table is full, or the stack is short -- then no
-// slot of the chunk grows) keeps its length, and its batch row ends before the
-// page its first new token would go to, so an append writes nothing.
+// The batch row of slot i gets the slot's page ids (entries past them are not
+// written: the kernels read a row only up to its length).  A slot that cannot
+// grow (its table is full, or the stack is short -- then no slot of the chunk
+// grows) keeps its length, and its batch row holds -1 from the page its first
+// new token would go to, so an append writes nothing.
+//
+// Order of work, to overlap the dependent memory round trips: lengths and tail
+// page ids; the copy of each row's existing entries (in flight while) the
+// reference-count checks, the prefix sum of the pages needed and the pops.
 __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
   __shared__ int s_wave[kWaves];
   __shared__ int s_top, s_fail, s_ncow;
-  __shared__ int s_slot[kThreads], s_keep[kThreads];
+  __shared__ int s_slot[kThreads], s_old[kThreads], s_base[kThreads];
   __shared__ int s_cow_src[kThreads], s_cow_dst[kThreads];
   const ArenaRefs r(a);
   const int P = a.page_tokens, mp = a.max_pages;
+  if (threadIdx.x == 0) s_top = *r.top;  // only this kernel moves it while it runs
   for (int c0 = 0; c0 < a.count; c0 += kThreads) {
     const int i = c0 + threadIdx.x;
-    int s = -1, w = 0, L = 0, nl = 0, oldp = 0, newp = 0, need = 0, tail = -1;
+    int s = -1, w = 0, L = 0, nl = 0, oldp = 0, need = 0, tail = -1;
     bool cow = false, blocked = false;
     if (i < a.count) {
       s = a.slots[i];
@@ -101,38 +108,75 @@ __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
           if (tail < 0 || tail >= a.capacity) {
             atomicOr(r.err, kArenaCorrupt);
             blocked = true;
-          } else if (atomicSub(&r.ref[tail], 1) > 1) {
-            cow = true;  // shared with another slot: write into a copy
-          } else {
-            atomicAdd(&r.ref[tail], 1);  // this slot holds the only reference
           }
         }
-        if (blocked) nl = L;
-        newp = cdiv(nl, P);
-        need = newp - oldp + (cow ? 1 : 0);
       }
     }
+    s_slot[threadIdx.x] = s;
+    s_old[threadIdx.x] = s >= 0 ? oldp : 0;
+    // the rows' existing entries: flattened copy (its loads stay in flight
+    // through the reference-count checks below)
+    const int rows = min(kThreads, a.count - c0);
+    {
+      int total_old;
+      const int incl_old = block_scan_incl(s >= 0 ? oldp : 0, s_wave, &total_old);
+      s_base[threadIdx.x] = incl_old - (s >= 0 ? oldp : 0);
+      __syncthreads();
+      for (int e0 = threadIdx.x; e0 < total_old; e0 += 4 * kThreads) {
+        int val[4];
+        int64_t dst[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * kThreads;
+          dst[u] = -1;
+          if (e < total_old) {
+            int lo = 0, hi = rows - 1;  // the last row whose base <= e
+            while (lo < hi) {
+              const int mid = (lo + hi + 1) >> 1;
+              if (s_base[mid] <= e) lo = mid; else hi = mid - 1;
+            }
+            const int p = e - s_base[lo];
+            dst[u] = (int64_t)(c0 + lo) * mp + p;
+            val[u] = a.table[(int64_t)s_slot[lo] * mp + p];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (dst[u] >= 0) a.batch_table[dst[u]] = val[u];
+      }
+    }
+    // copy-on-write decisions: a tail held by this slot alone is written in place
+    if (tail >= 0 && !blocked) {
+      if (r.ref[tail] > 1) {
+        if (atomicSub(&r.ref[tail], 1) > 1) cow = true;  // still shared: write into a copy
+        else atomicAdd(&r.ref[tail], 1);                 // the others let go meanwhile
+      }
+    }
+    if (blocked) nl = L;
+    const int newp = cdiv(nl, P);
+    need = s >= 0 ? newp - oldp + (cow ? 1 : 0) : 0;
     int total;
     const int incl = block_scan_incl(need, s_wave, &total);
     if (threadIdx.x == 0) {
-      s_top = *r.top;
       s_fail = s_top < total;
       if (s_fail) atomicOr(r.err, kArenaOutOfPages);
-      else *r.top = s_top - total;
       s_ncow = 0;
     }
     __syncthreads();
+    const int top = s_top;
     if (s >= 0 && s_fail && w > 0) {
       if (cow) atomicAdd(&r.ref[tail], 1);  // nothing taken: give the reference back
       blocked = true;
       nl = L;
     }
+    int64_t brow = (int64_t)i * mp;
     if (s >= 0 && !s_fail && !blocked) {
-      int pos = s_top - 1 - (incl - need);  // this slot's pages: stack[pos], stack[pos - 1], ...
+      int pos = top - 1 - (incl - need);  // this slot's pages: stack[pos], stack[pos - 1], ...
       if (cow) {
         const int np = r.stack[pos--];
         if (np >= 0 && np < a.capacity) {
           a.table[(int64_t)s * mp + L / P] = np;
+          a.batch_table[brow + L / P] = np;
           r.ref[np] = 1;
           const int k = atomicAdd(&s_ncow, 1);
           s_cow_src[k] = tail;
@@ -143,23 +187,23 @@ __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
       }
       for (int p = oldp; p < newp; ++p) {
         const int np = r.stack[pos--];
-        if (np >= 0 && np < a.capacity) {
-          a.table[(int64_t)s * mp + p] = np;
-          r.ref[np] = 1;
-        } else {
-          a.table[(int64_t)s * mp + p] = -1;
-          atomicOr(r.err, kArenaCorrupt);
-        }
+        const int id = np >= 0 && np < a.capacity ? np : -1;
+        if (id < 0) atomicOr(r.err, kArenaCorrupt);
+        else r.ref[id] = 1;
+        a.table[(int64_t)s * mp + p] = id;
+        a.batch_table[brow + p] = id;
       }
       a.lens[s] = nl;
+    } else if (s >= 0 && blocked && w > 0) {
+      // no page for the new tokens in the batch row: from the one the first goes to
+      for (int p = L / P; p < min(mp, cdiv(L + w, P)); ++p) a.batch_table[brow + p] = -1;
     }
     if (i < a.count) {
       a.batch_starts[i] = L;
       a.batch_lens[i] = nl;
     }
-    s_slot[threadIdx.x] = s;
-    s_keep[threadIdx.x] = blocked ? L / P : cdiv(nl, P);
     __syncthreads();
+    if (threadIdx.x == 0 && !s_fail) s_top = top - total;
     // copy-on-write: the shared tail's bytes into the new page, in every layer's pool
     const int64_t vecs = a.page_bytes / 16;
     for (int k = 0; k < s_ncow; ++k)
@@ -168,16 +212,9 @@ __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
         u4 *dst = (u4 *)(a.pools[l] + (int64_t)s_cow_dst[k] * a.page_bytes);
         for (int64_t v = threadIdx.x; v < vecs; v += kThreads) dst[v] = src[v];
       }
-    // the batch's block-table rows: the slot's pages, -1 past them
-    const int rows = min(kThreads, a.count - c0);
-    for (int64_t e = threadIdx.x; e < (int64_t)rows * mp; e += kThreads) {
-      const int row = (int)(e / mp), p = (int)(e - (int64_t)row * mp);
-      const int sl = s_slot[row];
-      a.batch_table[(int64_t)(c0 + row) * mp + p] =
-          sl >= 0 && p < s_keep[row] ? a.table[(int64_t)sl * mp + p] : -1;
-    }
-    __syncthreads();  // LDS reuse by the next chunk
+    __syncthreads();  // s_top and LDS reuse by the next chunk
   }
+  if (threadIdx.x == 0) *r.top = s_top;
 }
 
 // Per-item page ranges [from, to) of `count` items, flattened over the

@@ -40,7 +40,7 @@ class Reservation:
 
     slots: torch.Tensor        # [B] int32
     widths: torch.Tensor       # [B] int32 new tokens per slot
-    table: torch.Tensor        # [B, max_pages] int32 page ids, -1 past each slot's pages
+    table: torch.Tensor        # [B, max_pages] int32 page ids (entries past a slot's pages unset)
     starts: torch.Tensor       # [B] int32 length before the step (= the first new position)
     lens: torch.Tensor         # [B] int32 length after the step
 
