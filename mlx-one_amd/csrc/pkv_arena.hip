@@ -114,35 +114,43 @@ __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
     }
     s_slot[threadIdx.x] = s;
     s_old[threadIdx.x] = s >= 0 ? oldp : 0;
-    // the rows' existing entries: flattened copy (its loads stay in flight
-    // through the reference-count checks below)
+    // the rows' existing entries: flattened copy, four entries per item when
+    // rows are 16-byte aligned (max_pages % 4 == 0); its loads stay in flight
+    // through the reference-count checks below
     const int rows = min(kThreads, a.count - c0);
     {
-      int total_old;
-      const int incl_old = block_scan_incl(s >= 0 ? oldp : 0, s_wave, &total_old);
-      s_base[threadIdx.x] = incl_old - (s >= 0 ? oldp : 0);
+      const int V = mp % 4 == 0 ? 4 : 1;  // entries per item
+      const int items = s >= 0 ? cdiv(oldp, V) : 0;
+      int total_items;
+      const int incl_items = block_scan_incl(items, s_wave, &total_items);
+      s_base[threadIdx.x] = incl_items - items;
       __syncthreads();
-      for (int e0 = threadIdx.x; e0 < total_old; e0 += 4 * kThreads) {
-        int val[4];
+      for (int e0 = threadIdx.x; e0 < total_items; e0 += 4 * kThreads) {
+        u4 val[4];
         int64_t dst[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = e0 + u * kThreads;
           dst[u] = -1;
-          if (e < total_old) {
+          if (e < total_items) {
             int lo = 0, hi = rows - 1;  // the last row whose base <= e
             while (lo < hi) {
               const int mid = (lo + hi + 1) >> 1;
               if (s_base[mid] <= e) lo = mid; else hi = mid - 1;
             }
-            const int p = e - s_base[lo];
+            const int p = (e - s_base[lo]) * V;
             dst[u] = (int64_t)(c0 + lo) * mp + p;
-            val[u] = a.table[(int64_t)s_slot[lo] * mp + p];
+            const int32_t *src = a.table + (int64_t)s_slot[lo] * mp + p;
+            if (V == 4) val[u] = *(const u4 *)src;
+            else val[u].x = *src;
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (dst[u] >= 0) a.batch_table[dst[u]] = val[u];
+        for (int u = 0; u < 4; ++u) {
+          if (dst[u] < 0) continue;
+          if (V == 4) *(u4 *)(a.batch_table + dst[u]) = val[u];
+          else a.batch_table[dst[u]] = (int)val[u].x;
+        }
       }
     }
     // copy-on-write decisions: a tail held by this slot alone is written in place

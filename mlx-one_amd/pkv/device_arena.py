@@ -47,7 +47,8 @@ class Reservation:
 
 class DevicePageArena:
     """``capacity_pages`` pages of ``fmt`` in ``num_layers`` device pools, and
-    ``max_slots`` sequence slots of at most ``max_tokens`` tokens each."""
+    ``max_slots`` sequence slots of at most ``max_tokens`` tokens each (rounded
+    up to a whole multiple of four pages)."""
 
     def __init__(self, fmt, capacity_pages, *, num_layers=1, max_slots=64, max_tokens=8192,
                  device="cuda"):
@@ -58,7 +59,8 @@ class DevicePageArena:
         self.fmt = fmt
         self.capacity = int(capacity_pages)
         self.page_tokens = fmt.page_tokens
-        self.max_pages = -(-int(max_tokens) // self.page_tokens)
+        # rows of four-entry multiples: the reserve kernel copies them 16 bytes at a time
+        self.max_pages = -(-int(max_tokens) // (4 * self.page_tokens)) * 4
         self.max_slots = int(max_slots)
         self.device = torch.device(device)
         lib = nat.load()
