@@ -13,6 +13,14 @@ class CacheCapacityError(CacheError, MemoryError):
         self.retryable = retryable
 
 
+class CacheTopologyUnsupported(CacheError):
+    """The cache plan cannot serve the requested layer topology."""
+
+
+class PrefixReuseUnsupported(CacheError):
+    """Cached prefixes cannot be reused for this request."""
+
+
 class KVQuantizationUnsupported(CacheError):
     """A requested KV quantization/backend combination is unsupported."""
 

@@ -6,22 +6,28 @@ Same names and error behaviour for the calls the paged path makes:
 ``estimate_growth`` (the quantized growth formula of :255-262, with this
 build's group size in place of 32), ``reserve`` / ``commit`` / ``reconcile`` /
 ``release_reservation`` / ``transient_reservation`` (a byte budget; over budget
-raises ``CacheCapacityError``), ``release``, ``stats``, ``close``.  The arena
+raises ``CacheCapacityError``), ``fingerprint`` / ``adopt_prefix`` /
+``publish_prefix`` (shared prefix pages through ``BlockPrefixIndex``, :99-130,
+:415-497, :633-667), ``release``, ``stats``, ``close``.  The arena
 (``block_pool``) is a ``SegmentedPageArena`` whose pages live in device pools.
-Dense / block / hybrid backends, prefix indexing, quality qualification and
-host admission are outside the paged path and raise on use.
+Dense / block / hybrid backends, the cold (SSD) prefix store, quality
+qualification and host admission are outside the paged path.
 """
 
 from __future__ import annotations
 
+import hashlib
+import json
 import threading
 import uuid
 from contextlib import contextmanager
 from dataclasses import dataclass, field
 
 from pkv.arena import SegmentedPageArena
-from pkv.cache_errors import CacheCapacityError, CacheCorruptionError, KVQuantizationUnsupported
+from pkv.cache_errors import (CacheCapacityError, CacheCorruptionError, CacheTopologyUnsupported,
+                              KVQuantizationUnsupported, PrefixReuseUnsupported)
 from pkv.paged import PagedKVCache
+from pkv.prefix_cache import BlockPrefixIndex, CacheFingerprint
 
 _BITS = {"f16": None, "bf16": None, "q8_0": 8, "q4_0": 4}
 
@@ -35,6 +41,7 @@ class CacheConfig:
     memory_budget_bytes: int = 8 << 30
     group_size: int = 32
     prefix_cache_enabled: bool = False
+    prefix_cache_budget_bytes: int = 256 << 20
 
 
 @dataclass
@@ -92,6 +99,8 @@ class CacheManager:
         self.bundle, self.config = bundle, config
         self.block_pool = SegmentedPageArena(config.memory_budget_bytes,
                                              block_tokens=config.block_size_tokens, device=device)
+        self.block_prefix = BlockPrefixIndex(config.prefix_cache_budget_bytes,
+                                             block_tokens=config.block_size_tokens)
         self._lock = threading.RLock()
         self._handles = {}
         self._reserved = 0
@@ -145,6 +154,88 @@ class CacheManager:
                                                 "requested_output_tokens": max_new_tokens,
                                                 "total_growth_bytes": amount}
         return amount
+
+    # -- shared prefixes ------------------------------------------------------------------
+    def fingerprint(self, *, key_type="f16", value_type="f16", context_tokens=None,
+                    namespace=None, rendering_options=None, multimodal_identity=None):
+        """The reuse key of cached KV for this model and precision (``cache_manager.py:99-130``)."""
+        spec = self.bundle.spec
+        shape = [(s.layer_id, s.query_heads, s.kv_heads, s.key_dim) for s in spec.layers]
+        topology = hashlib.sha256(json.dumps(shape).encode()).hexdigest()
+        rope = json.dumps({"rope_theta": spec.rope_theta, "rope_scaling": spec.rope_scaling},
+                          sort_keys=True, default=str)
+        rendering = json.dumps(rendering_options or {}, sort_keys=True, default=str)
+        return CacheFingerprint(
+            model_id=str(getattr(self.bundle, "model_id", "pkv-attention-stack")),
+            revision=getattr(self.bundle, "revision", None),
+            model_identity=str(getattr(self.bundle, "model_identity", topology)),
+            adapter_identity=getattr(self.bundle, "adapter_identity", None),
+            tokenizer_identity=str(getattr(self.bundle, "tokenizer_identity", "")),
+            template_identity=str(getattr(self.bundle, "template_identity", "")),
+            topology_digest=topology, key_type=key_type, value_type=value_type,
+            context_tokens=int(context_tokens or 0), rope_identity=hashlib.sha256(
+                rope.encode()).hexdigest(),
+            namespace=namespace or "private",
+            rendering_identity=hashlib.sha256(rendering.encode()).hexdigest(),
+            multimodal_identity=multimodal_identity)
+
+    def adopt_prefix(self, handle, fingerprint, tokens, *, minimum_tokens=1):
+        """Give the handle the longest published prefix of ``tokens``; returns
+        the tokens reused (0 when none).  ``cache_manager.py:415-497``, paged branch."""
+        with self._lock:
+            self._validate_handle(handle)
+            handle.metadata["fingerprint"] = fingerprint
+            if fingerprint.multimodal_identity is not None:
+                raise PrefixReuseUnsupported("multimodal prefix restoration is unavailable")
+            if not self.config.prefix_cache_enabled:
+                return 0
+            match = self.block_prefix.lookup(fingerprint, tuple(tokens),
+                                             minimum_tokens=minimum_tokens)
+            if match is None:
+                return 0
+            if len(match.layer_references) != len(handle.bundle.entries):
+                for layer in match.layer_references:
+                    for ref in layer:
+                        ref.close()
+                raise CacheTopologyUnsupported("prefix layer count does not match cache plan")
+            staged = []
+            try:
+                for cache, refs in zip(handle.bundle.entries, match.layer_references, strict=True):
+                    draft = cache.empty()
+                    draft.adopt(list(refs))
+                    staged.append(draft)
+            except BaseException:
+                for draft in staged:
+                    draft.reset()
+                for layer in match.layer_references[len(staged):]:
+                    for ref in layer:
+                        if not ref.closed:
+                            ref.close()
+                raise
+            old = handle.bundle
+            handle.bundle = CacheBundle(tuple(staged))
+            for entry in old.entries:
+                entry.reset()
+            handle.token_count = match.token_count
+            handle.metadata["shared_blocks"] = match.block_count
+            handle.metadata["prefix_tokens_reused"] = match.token_count
+            return match.token_count
+
+    def publish_prefix(self, handle, fingerprint, tokens, *, maximum_entries=None):
+        """Index the handle's complete pages under ``tokens`` (the prompt it
+        holds); ``cache_manager.py:633-667``, paged branch."""
+        with self._lock:
+            self._validate_handle(handle)
+            if not self.config.prefix_cache_enabled or not tokens:
+                return False
+            if (handle.metadata.get("cancelled") or fingerprint.multimodal_identity is not None
+                    or any(int(c.offset) != len(tokens) for c in handle.bundle.entries)):
+                return False
+            layers = tuple(cache.full_block_refs for cache in handle.bundle.entries)
+            stored = self.block_prefix.publish(fingerprint, tuple(tokens), layers) > 0
+            handle.metadata["prefix_publications"] = (
+                handle.metadata.get("prefix_publications", 0) + int(stored))
+            return stored
 
     # -- byte budget -------------------------------------------------------------------
     def reserve(self, handle, nbytes):
@@ -223,5 +314,6 @@ class CacheManager:
         with self._lock:
             for handle in list(self._handles.values()):
                 self.release(handle)
+            self.block_prefix.clear()
             self.block_pool.clear()
             self._closed = True

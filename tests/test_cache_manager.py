@@ -142,3 +142,89 @@ def test_in_place_append_rolls_back_by_length():
     assert cm.block_pool.stats()["block_live"] == live_before
     cache._plan_append(6, layout)                # appends continue from the restored tail
     assert cache.offset == 16 and cache._blocks[0].block.immutable
+
+
+# ---------------------------------------------------------------- shared prefixes
+# BlockPrefixIndex / adopt_prefix / publish_prefix (engine/prefix_cache.py:186-348,
+# engine/cache_manager.py:415-497, :633-667), on the host bookkeeping alone.
+
+
+def _prefilled(cm, request_id, tokens):
+    h = cm.create_handle(request_id, key_type="q8_0", value_type="q8_0")
+    for cache in h.bundle.entries:
+        cache._plan_append(len(tokens), cache.layout_for(2, 64))
+    h.token_count = len(tokens)
+    return h
+
+
+def test_published_prefix_is_adopted_by_a_later_request():
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(1000, 1053))                    # 3 complete pages + 5 tokens
+    first = _prefilled(cm, "a", prompt)
+    assert cm.publish_prefix(first, fp, prompt)
+    assert cm.block_prefix.stats()["entries"] == 3
+    second = cm.create_handle("b", key_type="q8_0", value_type="q8_0")
+    assert cm.adopt_prefix(second, fp, prompt + (7, 8)) == 48
+    for mine, theirs in zip(second.bundle.entries, first.bundle.entries, strict=True):
+        assert mine.offset == 48
+        assert [r.block_id for r in mine._blocks] == [r.block_id for r in theirs._blocks[:3]]
+        assert all(r.block.references == 2 for r in mine._blocks)
+    # the publisher goes away: the index's pins keep the pages for the next request
+    cm.release(first)
+    third = cm.create_handle("c", key_type="q8_0", value_type="q8_0")
+    assert cm.adopt_prefix(third, fp, prompt) == 48
+    assert cm.block_prefix.stats()["hits"] == 2
+
+
+def test_prefix_lookup_stops_at_the_first_different_block_and_never_takes_the_last_token():
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(64))
+    cm.publish_prefix(_prefilled(cm, "a", prompt), fp, prompt)
+    index = cm.block_prefix
+    assert index.longest_prefix_tokens(fp, prompt) == 48            # last token stays
+    assert index.longest_prefix_tokens(fp, prompt + (1,)) == 64
+    changed = prompt[:20] + (999,) + prompt[21:]
+    assert index.longest_prefix_tokens(fp, changed) == 16
+    other = cm.fingerprint(key_type="q4_0", value_type="q4_0")
+    assert index.longest_prefix_tokens(other, prompt + (1,)) == 0
+    h = cm.create_handle("b", key_type="q8_0", value_type="q8_0")
+    assert cm.adopt_prefix(h, fp, prompt + (1,), minimum_tokens=80) == 0
+    assert index.stats()["misses"] == 1
+
+
+def test_prefix_index_evicts_leaves_under_its_budget():
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    page = cm.block_pool.pool_for(cm.create_handle("x", key_type="q8_0", value_type="q8_0")
+                                  .bundle.entries[0].layout_for(2, 64)).page_bytes
+    cm.block_prefix.capacity_bytes = 3 * 2 * page       # two blocks of three layers
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(49))
+    h = _prefilled(cm, "a", prompt)
+    assert cm.publish_prefix(h, fp, prompt)
+    stats = cm.block_prefix.stats()
+    assert stats["entries"] == 2 and stats["evictions"] == 1
+    assert cm.block_prefix.longest_prefix_tokens(fp, prompt) == 32   # the leaf went first
+    cm.release(h)
+    cm.block_prefix.clear()
+    assert cm.block_pool.nbytes == 0                     # unpinned pages were freed
+
+
+def test_prefix_reuse_rules():
+    from pkv.cache_errors import PrefixReuseUnsupported
+
+    cm = _manager(prefix_cache_enabled=False)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    h = _prefilled(cm, "a", tuple(range(40)))
+    assert cm.publish_prefix(h, fp, tuple(range(40))) is False
+    assert cm.adopt_prefix(cm.create_handle("b"), fp, tuple(range(40))) == 0
+    cm2 = _manager(prefix_cache_enabled=True)
+    mm = cm2.fingerprint(key_type="q8_0", value_type="q8_0", multimodal_identity="img")
+    with pytest.raises(PrefixReuseUnsupported):
+        cm2.adopt_prefix(cm2.create_handle("c"), mm, (1, 2, 3))
+    h2 = _prefilled(cm2, "d", tuple(range(40)))
+    assert cm2.publish_prefix(h2, mm, tuple(range(40))) is False
+    assert cm2.publish_prefix(h2, fp, tuple(range(39))) is False    # length must match
+    assert fp.digest == cm2.fingerprint(key_type="q8_0", value_type="q8_0").digest
+    assert fp.digest != cm2.fingerprint(key_type="q8_0", value_type="q8_0", namespace="x").digest

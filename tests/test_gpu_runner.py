@@ -201,3 +201,47 @@ def test_failed_step_leaves_caches_unchanged(copy_on_write):
     want = ref.step(hidden)
     for i in range(2):
         _close(out.logits[i][0].float().cpu().numpy(), want[i][-1:], 2e-2, 2e-3)
+
+
+def test_adopted_prefix_pages_give_the_same_steps_as_computed_ones():
+    """Request B adopts the prefix pages request A published; request C computes
+    the same prompt itself.  Same chunks, same shapes: B's and C's later steps
+    must agree bit for bit (the shared pages are A's, which equal C's)."""
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, device="cuda", seed=9)
+    cm = CacheManager(model, CacheConfig(block_size_tokens=16, key_type="q8_0", value_type="q8_0",
+                                         group_size=32, prefix_cache_enabled=True,
+                                         memory_budget_bytes=1 << 30))
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    runner = PagedRunner(model)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    prompt = tuple(range(500, 553))                          # 53 tokens: 3 pages + 5
+    hidden = torch.randn((53, 256), generator=gen, device="cuda").half()
+
+    def run(handle, x, phase):
+        return runner.execute([ForwardRequest(handle.request_id, x, handle.bundle.entries,
+                                              phase=phase, runtime=cm, handle=handle)])
+
+    a = cm.create_handle("a", key_type="q8_0", value_type="q8_0")
+    c = cm.create_handle("c", key_type="q8_0", value_type="q8_0")
+    for h in (a, c):
+        run(h, hidden[:48], "prefill")
+        run(h, hidden[48:], "prefill")
+    assert cm.publish_prefix(a, fp, prompt)
+    b = cm.create_handle("b", key_type="q8_0", value_type="q8_0")
+    assert cm.adopt_prefix(b, fp, prompt) == 48
+    assert [r.block_id for r in b.bundle.entries[0]._blocks] == \
+        [r.block_id for r in a.bundle.entries[0]._blocks[:3]]
+    run(b, hidden[48:], "prefill")
+    cm.release(a)                                            # B keeps A's pages alive
+    for _ in range(3):
+        x = torch.randn((1, 256), generator=gen, device="cuda").half()
+        out_b, out_c = run(b, x, "decode"), run(c, x, "decode")
+        torch.cuda.synchronize()
+        assert torch.equal(out_b.logits[0], out_c.logits[0])
+    assert b.token_count == c.token_count == 56
