@@ -245,3 +245,49 @@ def test_adopted_prefix_pages_give_the_same_steps_as_computed_ones():
         torch.cuda.synchronize()
         assert torch.equal(out_b.logits[0], out_c.logits[0])
     assert b.token_count == c.token_count == 56
+
+
+def test_snapshot_restore_gives_the_same_steps(tmp_path):
+    """A request's caches saved to disk and restored into a fresh arena take the
+    next steps exactly as the originals do; the reference-format export equals
+    gather_pages of the same pages."""
+    from pkv import ops
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+    from pkv.snapshot import load_snapshot, save_snapshot
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, device="cuda", seed=11)
+    config = CacheConfig(block_size_tokens=16, key_type="q4_0", value_type="q4_0", group_size=32,
+                         memory_budget_bytes=1 << 30)
+    cm, cm2 = CacheManager(model, config), CacheManager(model, config)
+    runner = PagedRunner(model)
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    a = cm.create_handle("a", key_type="q4_0", value_type="q4_0")
+    runner.execute([ForwardRequest("a", torch.randn((45, 256), generator=gen, device="cuda").half(),
+                                   a.bundle.entries, phase="prefill", runtime=cm, handle=a)])
+    manifest = save_snapshot(tmp_path, a.bundle, identity="m", reference_pages=True)
+    restored = load_snapshot(tmp_path, identity="m", expected_specs=cm2.layer_specs,
+                             page_pool=cm2.block_pool, bits=4)
+    b = cm2.create_handle("b", key_type="q4_0", value_type="q4_0")
+    for entry in b.bundle.entries:
+        entry.reset()
+    b.bundle = restored
+    b.token_count = restored.offset
+    # the reference-format pages in the payload, before any step writes more tokens
+    data = np.load(tmp_path / manifest["payload"])
+    cache = restored.entries[0]
+    pool = cache.pool.pool_for(cache.layout)
+    ids = torch.tensor([r.block.page for r in cache._blocks], dtype=torch.int32, device="cuda")
+    exported = ops.gather_pages(pool.fmt, pool.buffer, ids)
+    for name, value in zip(("k_codes", "k_scale", "k_bias", "v_codes", "v_scale", "v_bias"),
+                           exported, strict=True):
+        assert np.array_equal(data[f"layer_0_reference_{name}"], value.cpu().numpy()), name
+    for _ in range(3):
+        x = torch.randn((1, 256), generator=gen, device="cuda").half()
+        out_a = runner.execute([ForwardRequest("a", x, a.bundle.entries, runtime=cm, handle=a)])
+        out_b = runner.execute([ForwardRequest("b", x, b.bundle.entries, runtime=cm2, handle=b)])
+        torch.cuda.synchronize()
+        assert torch.equal(out_a.logits[0], out_b.logits[0])

@@ -1,0 +1,105 @@
+"""CPU: paged snapshots on disk (``pkv.snapshot``; the reference's
+``engine/components.py:317-530`` snapshot protocol with page-image storage).
+
+Round trip of page bytes, token counts and offsets into a fresh arena; the
+manifest is the commit point (payload digest, identity, layout and schema are
+checked before anything is allocated); an older payload is removed on the
+next save.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from pkv.cache_manager import CacheConfig, CacheManager
+from pkv.layer import ModelSpec
+from pkv.snapshot import load_snapshot, save_snapshot
+
+torch = pytest.importorskip("torch")
+
+
+class _Bundle:
+    def __init__(self, spec):
+        self.spec = spec
+        self.activation_dtype = spec.dtype
+
+
+def _manager():
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=3,
+                     dtype="float16")
+    return CacheManager(_Bundle(spec), CacheConfig(block_size_tokens=16, group_size=32),
+                        device="cpu")
+
+
+def _filled(cm, tokens, seed=0):
+    h = cm.create_handle("r", key_type="q8_0", value_type="q8_0")
+    rng = np.random.default_rng(seed)
+    for cache in h.bundle.entries:
+        layout = cache.layout_for(2, 64)
+        cache._plan_append(tokens, layout)
+        pool = cache.pool.pool_for(layout)
+        for ref in cache._blocks:
+            pool.buffer[ref.block.page] = torch.from_numpy(
+                rng.integers(0, 256, pool.page_bytes, dtype=np.uint8))
+    return h
+
+
+def _bytes(cache):
+    pool = cache.pool.pool_for(cache.layout)
+    return [pool.buffer[r.block.page].clone() for r in cache._blocks]
+
+
+@pytest.mark.parametrize("fmt", ["npz", "safetensors"])
+def test_round_trip_restores_pages_counts_and_offsets(tmp_path, fmt):
+    cm = _manager()
+    h = _filled(cm, 53)
+    manifest = save_snapshot(tmp_path, h.bundle, identity="model-a", tensor_format=fmt)
+    assert manifest["schema_version"] == "pkv-pages-v1" and len(manifest["layers"]) == 3
+    other = _manager()
+    restored = load_snapshot(tmp_path, identity="model-a", expected_specs=other.layer_specs,
+                             page_pool=other.block_pool, bits=8)
+    for mine, theirs in zip(restored.entries, h.bundle.entries, strict=True):
+        assert mine.offset == theirs.offset == 53 and mine.bits == 8
+        assert [r.block.token_count for r in mine._blocks] == [16, 16, 16, 5]
+        assert [r.block.immutable for r in mine._blocks] == [True, True, True, False]
+        assert all(torch.equal(a, b) for a, b in zip(_bytes(mine), _bytes(theirs), strict=True))
+        assert mine.page_table.pages == [r.block.page for r in mine._blocks]
+
+
+def test_manifest_is_checked_before_anything_is_allocated(tmp_path):
+    cm = _manager()
+    h = _filled(cm, 40)
+    manifest = save_snapshot(tmp_path, h.bundle, identity="model-a")
+    other = _manager()
+    with pytest.raises(ValueError, match="identity"):
+        load_snapshot(tmp_path, identity="model-b", expected_specs=other.layer_specs,
+                      page_pool=other.block_pool)
+    with pytest.raises(ValueError, match="layout"):
+        load_snapshot(tmp_path, identity="model-a", expected_specs=other.layer_specs,
+                      page_pool=other.block_pool, bits=4)
+    payload = tmp_path / manifest["payload"]
+    data = bytearray(payload.read_bytes())
+    data[len(data) // 2] ^= 0xFF
+    payload.write_bytes(bytes(data))
+    with pytest.raises(ValueError, match="digest"):
+        load_snapshot(tmp_path, identity="model-a", expected_specs=other.layer_specs,
+                      page_pool=other.block_pool)
+    assert other.block_pool.nbytes == 0
+
+
+def test_a_new_save_replaces_the_payload_and_empty_caches_round_trip(tmp_path):
+    cm = _manager()
+    first = save_snapshot(tmp_path, _filled(cm, 20).bundle, identity="m")
+    empty = cm.create_handle("e", key_type="q8_0", value_type="q8_0")
+    second = save_snapshot(tmp_path, empty.bundle, identity="m")
+    assert not (tmp_path / first["payload"]).exists() and (tmp_path / second["payload"]).exists()
+    assert json.loads((tmp_path / "state.json").read_text())["payload"] == second["payload"]
+    other = _manager()
+    restored = load_snapshot(tmp_path, identity="m", expected_specs=other.layer_specs,
+                             page_pool=other.block_pool, bits=8, dtype="float16")
+    assert [c.offset for c in restored.entries] == [0, 0, 0]
+    with pytest.raises(ValueError):
+        save_snapshot(tmp_path, [], identity="m")
