@@ -42,6 +42,10 @@ class CacheConfig:
     group_size: int = 32
     prefix_cache_enabled: bool = False
     prefix_cache_budget_bytes: int = 256 << 20
+    ssd_cache_directory: str | None = None
+    ssd_cache_budget_bytes: int = 1 << 30
+    ssd_staging_budget_bytes: int = 256 << 20
+    ssd_max_entries: int = 128
 
 
 @dataclass
@@ -101,6 +105,14 @@ class CacheManager:
                                              block_tokens=config.block_size_tokens, device=device)
         self.block_prefix = BlockPrefixIndex(config.prefix_cache_budget_bytes,
                                              block_tokens=config.block_size_tokens)
+        self.cold_prefix = None
+        if config.ssd_cache_directory:
+            from pkv.cold_prefix import ColdPrefixStore
+
+            self.cold_prefix = ColdPrefixStore(config.ssd_cache_directory,
+                                               budget_bytes=config.ssd_cache_budget_bytes,
+                                               staging_bytes=config.ssd_staging_budget_bytes,
+                                               max_entries=config.ssd_max_entries)
         self._lock = threading.RLock()
         self._handles = {}
         self._reserved = 0
@@ -192,7 +204,7 @@ class CacheManager:
             match = self.block_prefix.lookup(fingerprint, tuple(tokens),
                                              minimum_tokens=minimum_tokens)
             if match is None:
-                return 0
+                return self._adopt_cold(handle, fingerprint, tokens, minimum_tokens)
             if len(match.layer_references) != len(handle.bundle.entries):
                 for layer in match.layer_references:
                     for ref in layer:
@@ -235,7 +247,37 @@ class CacheManager:
             stored = self.block_prefix.publish(fingerprint, tuple(tokens), layers) > 0
             handle.metadata["prefix_publications"] = (
                 handle.metadata.get("prefix_publications", 0) + int(stored))
-            return stored
+            return self._publish_cold(handle, fingerprint, tokens) or stored
+
+    def _adopt_cold(self, handle, fingerprint, tokens, minimum):
+        """Restore the longest on-disk prefix into fresh pages (``cache_manager.py:499-540``)."""
+        if self.cold_prefix is None:
+            return 0
+        with self.transient_reservation(self.cold_prefix.staging):
+            bits = {e.bits for e in handle.bundle.entries}
+            match = self.cold_prefix.lookup(fingerprint, tuple(tokens), self.layer_specs,
+                                            page_pool=self.block_pool, minimum=minimum,
+                                            bits=bits.pop() if len(bits) == 1 else None)
+            if match is None:
+                return 0
+            count, restored = match
+            old = handle.bundle
+            handle.bundle = restored
+            for entry in old.entries:
+                entry.reset()
+            handle.token_count = count
+            handle.metadata["cold_prefix_tokens"] = count
+            return count
+
+    def _publish_cold(self, handle, fingerprint, tokens):
+        """Keep the handle's caches on disk as well (``cache_manager.py:541-559``).
+        Page images are stored, so quantized caches qualify too."""
+        if self.cold_prefix is None:
+            return False
+        return self.cold_prefix.put(fingerprint, tokens, handle.bundle,
+                                    page_tokens=self.config.block_size_tokens,
+                                    cancelled=lambda: bool(handle.closed or
+                                                           handle.metadata.get("cancelled")))
 
     # -- byte budget -------------------------------------------------------------------
     def reserve(self, handle, nbytes):

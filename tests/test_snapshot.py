@@ -103,3 +103,57 @@ def test_a_new_save_replaces_the_payload_and_empty_caches_round_trip(tmp_path):
     assert [c.offset for c in restored.entries] == [0, 0, 0]
     with pytest.raises(ValueError):
         save_snapshot(tmp_path, [], identity="m")
+
+
+# ---------------------------------------------------------------- cold prefix tier
+# ColdPrefixStore and the manager's fallback to it (engine/cold_prefix.py:93-240,
+# engine/cache_manager.py:499-559).
+
+
+def _cold_manager(directory, **kw):
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=3,
+                     dtype="float16")
+    config = CacheConfig(block_size_tokens=16, group_size=32, prefix_cache_enabled=True,
+                         ssd_cache_directory=str(directory), **kw)
+    return CacheManager(_Bundle(spec), config, device="cpu")
+
+
+def test_cold_tier_restores_a_prefix_another_manager_published(tmp_path):
+    cm = _cold_manager(tmp_path)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(300, 353))                      # 53 tokens
+    h = _filled(cm, 53)
+    h.token_count = 53
+    assert cm.publish_prefix(h, fp, prompt)
+    assert cm.cold_prefix.stats()["entries"] == 1
+    fresh = _cold_manager(tmp_path)                     # empty in-memory index: disk only
+    g = fresh.create_handle("g", key_type="q8_0", value_type="q8_0")
+    assert fresh.adopt_prefix(g, fp, prompt[:40] + (1, 2, 3)) == 32   # page-aligned match
+    for mine, theirs in zip(g.bundle.entries, h.bundle.entries, strict=True):
+        assert mine.offset == 32
+        assert all(torch.equal(a, b) for a, b in zip(_bytes(mine), _bytes(theirs)[:2], strict=True))
+    assert fresh.cold_prefix.stats()["hits"] == 1
+    other = fresh.fingerprint(key_type="q8_0", value_type="q8_0", namespace="tenant-b")
+    assert fresh.adopt_prefix(fresh.create_handle("x", key_type="q8_0", value_type="q8_0"),
+                              other, prompt) == 0
+
+
+def test_cold_tier_budget_and_corruption(tmp_path):
+    cm = _cold_manager(tmp_path, ssd_max_entries=2)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    for n in range(3):
+        h = _filled(cm, 20 + n, seed=n)
+        cm.publish_prefix(h, fp, tuple(range(n * 100, n * 100 + 20 + n)))
+        cm.release(h)
+    store = cm.cold_prefix
+    assert store.stats()["entries"] == 2                 # the oldest left
+    assert len([p for p in tmp_path.iterdir() if p.is_dir()]) == 2
+    assert store.preview(fp, tuple(range(0, 21)) + (9,)) == 0
+    assert store.preview(fp, tuple(range(200, 222)) + (9,)) == 16
+    index = json.loads((tmp_path / "index.json").read_text())
+    gen = tmp_path / index["entries"][-1]["generation"]
+    (gen / "state.json").write_text((gen / "state.json").read_text() + " ")
+    with pytest.raises(ValueError, match="checksum"):
+        store.lookup(fp, tuple(range(200, 222)) + (9,), cm.layer_specs, page_pool=cm.block_pool)
+    store.clear()
+    assert store.stats()["entries"] == 0 and not [p for p in tmp_path.iterdir() if p.is_dir()]
