@@ -407,7 +407,7 @@ def main(argv=None):
     parser.add_argument("--layers", type=int, default=4)
     parser.add_argument("--waves", type=int, default=0,
                         help="attention work waves (0: the workload's partition size, else the "
-                             "device's resident capacity)")
+                             "library default for the shape and batch)")
     parser.add_argument("--graph", action="store_true",
                         help="replay the timed steps as one captured HIP graph")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
@@ -450,8 +450,8 @@ def main(argv=None):
 
     context = inst.context.astype(np.int64)
     scale = 1.0 / math.sqrt(w.head_dim)
-    waves = args.waves or workload_waves(w, context + w.append_tokens) or ops.attention_waves(
-        fmt, w.heads, w.num_queries)
+    waves = args.waves or workload_waves(w, context + w.append_tokens) or ops.default_waves(
+        fmt, w.heads, w.num_queries, w.batch)
     # per-step device arrays (no host->device copies inside the timed loop)
     plans = []
     for s in range(total_steps):

@@ -107,7 +107,7 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
  *                 when t <= q_pos (paged_attention.py:81)
  *  widths       : [batch] real query rows (rows q >= widths[b] output 0), or NULL
  *  scale        : softmax scale
- *  waves        : work waves; <= 0 picks pkv_attention_waves(...)
+ *  waves        : work waves; <= 0 picks pkv_attention_default_waves(...)
  *  workspace    : device scratch of pkv_attention_workspace_bytes(...) bytes
  *                 (calls sharing one workspace must not overlap)
  *  out          : [batch][num_heads][num_queries][head_dim], float_kind
@@ -120,9 +120,16 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
                         int64_t workspace_bytes, void *out);
 
 /* Waves the attention kernel keeps resident on the current device for this
- * layout and (num_heads, num_queries): the default `waves` (1 for query
- * blocks served by the prefill kernel).  <0 on error. */
+ * layout and (num_heads, num_queries) (1 for query blocks served by the
+ * prefill kernel).  <0 on error. */
 int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries);
+
+/* The `waves` pkv_paged_attention uses when given waves <= 0: the resident
+ * waves, or half of them (one per SIMD) for decode rows (<= 4 query rows per
+ * KV head) when the batch has at most a quarter as many (sequence, KV head)
+ * segments as resident waves.  <0 on error. */
+int32_t pkv_attention_default_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries,
+                                    int32_t batch);
 
 /* Workspace bytes pkv_paged_attention needs for `waves` work waves (0 for
  * query blocks served by the prefill kernel). */

@@ -145,6 +145,21 @@ int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t
   return w;
 }
 
+int32_t pkv_attention_default_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries,
+                                    int32_t batch) {
+  const int32_t resident = pkv_attention_waves(layout, num_heads, num_queries);
+  if (resident <= 1 || batch < 1) return resident;
+  pkv_geometry g;
+  geometry(layout, &g);
+  const int64_t rows = (int64_t)num_queries * (num_heads / g.hk);
+  // Decode rows (<= 4 per KV head: four tiles per iteration) of a batch with
+  // few (sequence, KV head) segments: one wave per SIMD streams longer runs
+  // with fewer pieces to merge and measures faster; with many segments, two
+  // waves per SIMD keep more of them in flight.
+  if (rows <= 4 && (int64_t)batch * g.hk * 4 <= resident) return std::max(1, resident / 2);
+  return resident;
+}
+
 int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
                                       int32_t num_queries, int32_t waves) {
   pkv_geometry g;
@@ -209,7 +224,7 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
     return check_launch(pkv::launch_prefill((hipStream_t)stream, a), "prefill launch");
   }
   if (waves <= 0) {
-    waves = cached_waves(geo, rows);
+    waves = pkv_attention_default_waves(layout, num_heads, num_queries, batch);
     if (waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
   }
   if (waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");

@@ -39,6 +39,7 @@ SIGNATURES = {
     "pkv_paged_attention": ([_c_p, _LP, _c_p, _i64, _c_p, _i32, _i32, _i32, _c_p, _i32, _c_p,
                              _c_p, _c_p, _f32, _i32, _c_p, _i64, _c_p], ctypes.c_int),
     "pkv_attention_waves": ([_LP, _i32, _i32], _i32),
+    "pkv_attention_default_waves": ([_LP, _i32, _i32, _i32], _i32),
     "pkv_attention_workspace_bytes": ([_LP, _i32, _i32, _i32], _i64),
     "pkv_gather_pages": ([_c_p, _LP, _c_p, _i64, _c_p, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
                          ctypes.c_int),

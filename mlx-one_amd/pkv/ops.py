@@ -121,6 +121,15 @@ def attention_waves(fmt: PageFormat, num_heads, num_queries):
     return waves
 
 
+def default_waves(fmt: PageFormat, num_heads, num_queries, batch):
+    """The waves ``paged_attention`` uses by default for this shape and batch."""
+    waves = int(nat.load().pkv_attention_default_waves(fmt.c_layout, num_heads, num_queries,
+                                                         batch))
+    if waves <= 0:
+        nat.check(nat.PKV_LAUNCH_FAILED, "attention waves")
+    return waves
+
+
 def workspace_bytes(fmt: PageFormat, num_heads, num_queries, waves):
     return int(nat.load().pkv_attention_workspace_bytes(fmt.c_layout, num_heads, num_queries,
                                                           waves))
@@ -147,7 +156,7 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
 
     ``seq_lens`` counts the tokens in each sequence's cache (after the
     append) and stays on the device: the decode kernel shares the tiles of
-    all sequences out over ``waves`` waves (default: the resident capacity);
+    all sequences out over ``waves`` waves (default: ``default_waves``);
     query blocks past 32 rows per KV head run on the prefill kernel.
     ``workspace`` (bytes from ``workspace_bytes``) may be given by the caller.
     """
@@ -161,7 +170,7 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     table = _i32(block_table, device)
     lens = _i32(seq_lens, device)
     if waves <= 0:
-        waves = attention_waves(fmt, heads, nq)
+        waves = default_waves(fmt, heads, nq, batch)
     need = workspace_bytes(fmt, heads, nq, waves)
     if need < 0:
         nat.check(nat.PKV_INVALID_ARGUMENT, "paged attention workspace")

@@ -154,7 +154,7 @@ def test_workload_waves():
 
     c3 = workloads.get("c3")
     assert bench.workload_waves(c3, [32768] * 8) == 8 * 64 * 4
-    assert bench.workload_waves(workloads.get("c2"), [5000] * 32) == 0   # device capacity
+    assert bench.workload_waves(workloads.get("c2"), [5000] * 32) == 0   # library default
 
 
 def test_prefill_flops_match_the_causal_count():
