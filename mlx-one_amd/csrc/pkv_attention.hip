@@ -134,17 +134,17 @@ __device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int h
 }
 
 // Log-sum-exp merge of partition partials (paged_attention.py:191-204, in
-// the exp2 domain): one 4-wave workgroup per (segment, query row) of a segment
-// split over several waves' runs; whole segments were written by the
-// attention kernel.  Every wave finds M = max m and S = sum l 2^(m - M) over
-// the pieces (lanes stride the pieces); then wave w takes pieces w, w+4, ...,
-// with up to 16 partial rows in flight at once (lanes stride the DP columns),
-// and the four sums meet in LDS.  The merge is thus two memory round trips
-// whatever the number of pieces up to 64.
-template <int DP>
-__global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
+// the exp2 domain): one NW-wave workgroup (4, or 2 when there are so many
+// units that 4-wave groups would not all be resident) per (segment, query
+// row) of a segment split over several waves' runs; whole segments were
+// written by the attention kernel.  Every wave finds M = max m and
+// S = sum l 2^(m - M) over the pieces (lanes stride the pieces); then wave w
+// takes pieces w, w+NW, ..., with up to 16 partial rows in flight at once
+// (lanes stride the DP columns), and the NW sums meet in LDS.  The merge is
+// thus two memory round trips whatever the number of pieces up to 16*NW.
+template <int DP, int NW>
+__global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   constexpr int PER = DP / 64 > 0 ? DP / 64 : 1;  // output columns per lane
-  constexpr int NW = 4;                           // waves per workgroup
   constexpr int KW = 16;                          // pieces per wave in flight
   __shared__ float s_acc[NW - 1][64 * PER];
   const int lane = threadIdx.x & 63;
@@ -241,7 +241,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
     const int d = lane * PER + e;
-    const float v = acc[e] + s_acc[0][d] + s_acc[1][d] + s_acc[2][d];
+    float v = acc[e];
+#pragma unroll
+    for (int k = 0; k < NW - 1; ++k) v += s_acc[k][d];
     if (d < a.dim) o[d] = float_to_bits(v, a.float_kind);
   }
 }
@@ -830,16 +832,25 @@ hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
   return hipGetLastError();
 }
 
+constexpr int64_t kMergeResidentWaves = 8192;
+
 hipError_t launch_merge(hipStream_t stream, const MergeArgs &a) {
   const int64_t units = (int64_t)a.batch * a.hk * a.rows;  // one workgroup per (segment, row)
   if (units == 0 || a.waves <= 1) return hipSuccess;  // one run covers every segment whole
   if (units > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)units), block(256);
-  if (a.dp == 64) hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, stream, a);
-  else if (a.dp == 128) hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, stream, a);
-  else if (a.dp == 256) hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, stream, a);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  // Two-wave workgroups when four-wave ones would not all be resident at once
+  // (about 8,192 waves on the device), so the merge runs in one round.
+  const bool narrow = units * 4 > kMergeResidentWaves;
+  const dim3 grid((unsigned)units), block(narrow ? 128 : 256);
+#define PKV_M(DP_)                                                                         \
+  if (a.dp == DP_) {                                                                       \
+    if (narrow) hipLaunchKernelGGL((merge_kernel<DP_, 2>), grid, block, 0, stream, a);     \
+    else hipLaunchKernelGGL((merge_kernel<DP_, 4>), grid, block, 0, stream, a);            \
+    return hipGetLastError();                                                              \
+  }
+  PKV_M(64) PKV_M(128) PKV_M(256)
+#undef PKV_M
+  return hipErrorInvalidValue;
 }
 
 }  // namespace pkv
