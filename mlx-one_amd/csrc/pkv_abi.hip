@@ -193,7 +193,8 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   if (num_pages < 1 || max_pages < 1) return fail(PKV_INVALID_ARGUMENT, "empty page pool or block table");
   if (!std::isfinite(scale)) return fail(PKV_INVALID_ARGUMENT, "softmax scale must be finite");
   // the kernels number 16-token tiles in int32: bound them by the block table
-  const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16);
+  // (plus the split's lead tiles per segment)
+  const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16) + 16;
   if ((int64_t)batch * tiles_per_seq * geo.hk > INT32_MAX / 2)
     return fail(PKV_UNSUPPORTED, "paged attention batch too large (more than 2^30 tiles)");
   if (!pkv::decode_serves(pkv::to_geo(geo), rows)) {
@@ -218,6 +219,7 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
     a.widths = widths;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.waves = 0;
+    a.lead = 0;
     a.part_ml = nullptr;
     a.part_acc = nullptr;
     a.out = (uint16_t *)out;
@@ -250,6 +252,7 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   a.widths = widths;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.waves = waves;
+  a.lead = pkv::attention_lead(a.g, rows);
   a.part_ml = (float *)((char *)workspace + parts.ml);
   a.part_acc = (float *)((char *)workspace + parts.acc);
   a.out = (uint16_t *)out;
@@ -265,6 +268,7 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   m.dp = geo.dp;
   m.float_kind = geo.float_kind;
   m.waves = waves;
+  m.lead = a.lead;
   m.seq_lens = seq_lens;
   m.part_acc = a.part_acc;
   m.part_ml = a.part_ml;

@@ -8,9 +8,11 @@
 // Work split (stream-K).  The 16-token tiles of every (sequence, KV head)
 // segment, in that order, are shared out as equal contiguous runs over a grid
 // of resident waves (one 64-thread workgroup each): no wave waits on a ragged
-// tail and each pays its start-up latency once.  A wave processes the pieces
-// of the segments its run crosses; all R = Q*(H/HK) query rows of the KV head
-// share each K/V tile load (GQA reuse).
+// tail and each pays its start-up latency once.  The split counts `lead`
+// extra tiles ahead of each segment for the cost of starting a piece, so a
+// run that crosses into another segment holds fewer real tiles.  A wave
+// processes the pieces of the segments its run crosses; all R = Q*(H/HK)
+// query rows of the KV head share each K/V tile load (GQA reuse).
 //
 // Column slots.  The 16 columns of a 16x16 MFMA tile hold SLOTS = 16/RPS
 // groups of RPS query rows; slot j of an iteration works on tile (SLOTS*it +
@@ -87,11 +89,12 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-// Work split.  Tiles are numbered over (sequence b, KV head kh, tile t) in
-// that order, T in all; the tiles of one (b, kh) form a segment.  Wave w of W
-// (W <= T) owns the run [start(w), start(w+1)): equal runs whatever the
-// lengths, so no wave waits on a ragged tail and each pays its start-up once.
-// A run is cut into pieces at segment boundaries.
+// Work split.  Split tiles are numbered over (sequence b, KV head kh) in that
+// order, T in all: each (b, kh) segment spans `lead` tiles with no data, then
+// its own tiles.  Wave w of W (W <= T) owns the run [start(w), start(w+1)):
+// equal runs whatever the lengths, so no wave waits on a ragged tail and each
+// pays its start-up once.  A run is cut into pieces at segment boundaries; a
+// run that holds lead tiles only has no piece.
 struct Split {
   int T, W, q, r;  // T tiles over W waves: the first r runs have q + 1 tiles, the rest q
   __device__ __forceinline__ void init(int t, int w) {
@@ -107,19 +110,19 @@ struct Split {
 
 // Partial slots: the first piece of wave w's run goes to slot 2w, a later
 // (its last) one to 2w+1; pieces in between cover whole segments and write
-// the output directly.  The pieces of segment [s0, s1) are those of waves
-// wa .. wa+n-1; wave wa's piece is its first one unless its run started
-// before s0.
+// the output directly.  A segment starting at split tile sv has its tiles at
+// [s0, s1) (s0 = sv + lead); its pieces are those of waves wa .. wa+n-1, and
+// wave wa's piece is its first one unless its run started before sv.
 struct SegPieces {
   int n, wa, slot0;
   __device__ __forceinline__ int slot(int i) const { return i == 0 ? slot0 : 2 * (wa + i); }
 };
 
-__device__ __forceinline__ SegPieces seg_pieces(const Split &sp, int s0, int s1) {
+__device__ __forceinline__ SegPieces seg_pieces(const Split &sp, int sv, int s0, int s1) {
   SegPieces p;
   p.wa = sp.wave_of(s0);
   p.n = sp.wave_of(s1 - 1) - p.wa + 1;
-  p.slot0 = sp.start(p.wa) < s0 ? 2 * p.wa + 1 : 2 * p.wa;
+  p.slot0 = sp.start(p.wa) < sv ? 2 * p.wa + 1 : 2 * p.wa;
   return p;
 }
 
@@ -133,15 +136,34 @@ __device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int h
   return __builtin_amdgcn_readfirstlane(t) * hk;
 }
 
+// The lead tiles a launch's split charges ahead of each segment: `lead`, or
+// none when the lead-free split's equal runs already end on segment
+// boundaries (every sequence's tile count a multiple of the run length), so
+// that no run crosses one.  nt0: the lane's tile count in the first
+// 64-sequence chunk; t0: the lead-free tile total over all segments.
+__device__ __forceinline__ int charged_lead(const int32_t *lens, int batch, int waves, int lead,
+                                            int nt0, int t0, int lane) {
+  if (lead == 0) return 0;
+  const int w0 = min(waves, t0);
+  if (t0 % w0) return lead;
+  const int q0 = t0 / w0;
+  bool off = lane < batch && nt0 % q0 != 0;
+  for (int c0 = 64; c0 < batch; c0 += 64) {
+    const int idx = c0 + lane;
+    off |= idx < batch && seq_tiles(lens[idx]) % q0 != 0;
+  }
+  return __any(off) ? lead : 0;
+}
+
 // Log-sum-exp merge of partition partials (paged_attention.py:191-204, in
 // the exp2 domain): one NW-wave workgroup (4, or 2 when there are so many
 // units that 4-wave groups would not all be resident) per (segment, query
 // row) of a segment split over several waves' runs; whole segments were
 // written by the attention kernel.  Every wave finds M = max m and
-// S = sum l 2^(m - M) over the pieces (lanes stride the pieces); then wave w
-// takes pieces w, w+NW, ..., with up to 16 partial rows in flight at once
-// (lanes stride the DP columns), and the NW sums meet in LDS.  The merge is
-// thus two memory round trips whatever the number of pieces up to 16*NW.
+// S = sum l 2^(m - M) over the pieces (lanes stride the pieces); wave w
+// weighs pieces w, w+NW, ..., whose partial rows (lanes stride the DP
+// columns, up to 16 in flight) it requests before that pass, and the NW sums
+// meet in LDS.  Up to 16*NW pieces the merge is one memory round trip.
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   constexpr int PER = DP / 64 > 0 ? DP / 64 : 1;  // output columns per lane
@@ -153,49 +175,27 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   const int row = unit % a.rows, seg = unit / a.rows;
   const int b = seg / a.hk, kh = seg % a.hk;
   // tiles before sequence b, and the launch's split (as the attention kernel made it)
-  int pre = 0, tiles = 0;
+  int pre = 0, tiles = 0, nt0 = 0;
   for (int c0 = 0; c0 < a.batch; c0 += 64) {
     const int idx = c0 + lane;
     const int nt = idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0;
+    if (c0 == 0) nt0 = nt;
     tiles += wave_sum(nt);
     pre += wave_sum(idx < b ? nt : 0);
   }
-  const int T = __builtin_amdgcn_readfirstlane(tiles) * a.hk;
+  const int t0 = __builtin_amdgcn_readfirstlane(tiles) * a.hk;
+  const int lead = charged_lead(a.seq_lens, a.batch, a.waves, a.lead, nt0, t0, lane);
+  const int T = t0 + a.batch * a.hk * lead;
   const int ntb = seq_tiles(a.seq_lens[b]);
-  const int s0 = __builtin_amdgcn_readfirstlane(pre) * a.hk + kh * ntb;
+  const int sv = (__builtin_amdgcn_readfirstlane(pre) + b * lead) * a.hk + kh * (ntb + lead);
   Split sp;
   sp.init(T, min(a.waves, T));
-  const SegPieces pc = seg_pieces(sp, s0, s0 + ntb);
+  const SegPieces pc = seg_pieces(sp, sv, sv + lead, sv + lead + ntb);
   if (pc.n < 2) return;  // the same for every wave of the workgroup
 
-  // M = max m, S = sum l 2^(m - M) over the pieces (lanes stride the pieces)
-  float mx = -INFINITY, sm = 0.0f;
-  for (int k0 = 0; k0 < pc.n; k0 += 64) {
-    const int k = k0 + lane;
-    if (k < pc.n) {
-      const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
-      if (ml.y > 0.0f) {  // a piece with no visible token holds l = 0
-        const float nm = fmaxf(mx, ml.x);
-        sm = sm * __builtin_amdgcn_exp2f(mx - nm) + ml.y * __builtin_amdgcn_exp2f(ml.x - nm);
-        mx = nm;
-      }
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sm, o, 64);
-    const float nm = fmaxf(mx, om);
-    sm = nm == -INFINITY ? 0.0f
-                         : sm * __builtin_amdgcn_exp2f(mx - nm) + os * __builtin_amdgcn_exp2f(om - nm);
-    mx = nm;
-  }
-  const float inv = 1.0f / fmaxf(sm, 1e-20f);
-  float acc[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) acc[i] = 0.0f;
-  for (int k0 = 0; k0 < pc.n; k0 += NW * KW) {
-    // this wave's pieces k0 + wv + 4i: their partial rows, all requested at once
-    float x[KW][PER];
+  // this wave's partial rows of pieces k0 + wv + NW*i, all requested at once
+  float x[KW][PER];
+  auto request = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
       const int k = k0 + wv + NW * i;
@@ -214,9 +214,47 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
         }
       }
     }
-    // lane l: weight 2^(m - M) / S of piece k0 + l
-    float wl = 0.0f;
-    {
+  };
+  // The first rows go out before the (m, l) pass: both in one memory round trip.
+  request(0);
+
+  // M = max m, S = sum l 2^(m - M) over the pieces (lanes stride the pieces);
+  // lane l keeps piece l's (m, l)
+  float mx = -INFINITY, sm = 0.0f;
+  float2 mine = make_float2(-INFINITY, 0.0f);
+  for (int k0 = 0; k0 < pc.n; k0 += 64) {
+    const int k = k0 + lane;
+    if (k < pc.n) {
+      const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
+      if (k0 == 0) mine = ml;
+      if (ml.y > 0.0f) {  // a piece with no visible token holds l = 0
+        const float nm = fmaxf(mx, ml.x);
+        sm = sm * __builtin_amdgcn_exp2f(mx - nm) + ml.y * __builtin_amdgcn_exp2f(ml.x - nm);
+        mx = nm;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sm, o, 64);
+    const float nm = fmaxf(mx, om);
+    sm = nm == -INFINITY ? 0.0f
+                         : sm * __builtin_amdgcn_exp2f(mx - nm) + os * __builtin_amdgcn_exp2f(om - nm);
+    mx = nm;
+  }
+  const float inv = 1.0f / fmaxf(sm, 1e-20f);
+  // lane l: weight 2^(m - M) / S of piece l
+  const float w_first = mine.y > 0.0f ? __builtin_amdgcn_exp2f(mine.x - mx) * inv : 0.0f;
+  float acc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc[i] = 0.0f;
+  for (int k0 = 0; k0 < pc.n; k0 += NW * KW) {
+    if (k0 > 0) request(k0);
+    // lane l: weight of piece k0 + l (pieces below 64 from the pass above)
+    const bool held = k0 + NW * KW <= 64;
+    float wl = w_first;
+    if (!held) {
+      wl = 0.0f;
       const int k = k0 + lane;
       if (k < pc.n) {
         const float2 ml = *(const float2 *)(a.part_ml + ((int64_t)pc.slot(k) * a.rows + row) * 2);
@@ -225,7 +263,8 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
-      const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), wv + NW * i));
+      const int src_lane = held ? k0 + wv + NW * i : wv + NW * i;
+      const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), src_lane));
 #pragma unroll
       for (int e = 0; e < PER; ++e) acc[e] += wk * x[i][e];
     }
@@ -281,30 +320,38 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 
   // ---- sequences: lanes hold one 64-sequence chunk (length, tiles, inclusive
   // tile prefix over all sequences); chunk_pre / chunk_end bound its prefix
-  int cbase = 0, len_l = 0, nt_l = 0, incl_l = 0, chunk_pre = 0, chunk_end = 0;
-  auto load_chunk = [&](int base, int pre) __attribute__((always_inline)) {
+  int cbase = 0, len_l = 0, nt_l = 0, incl_l = 0, chunk_pre = 0, chunk_end = 0, lead = 0;
+  auto scan_chunk = [&](int base, int pre) __attribute__((always_inline)) {
     cbase = base;
     chunk_pre = pre;
+    incl_l = wave_scan_incl(base + lane < a.batch ? nt_l + lead : 0, lane) + pre;
+    chunk_end = __builtin_amdgcn_readlane(incl_l, 63);
+  };
+  auto load_chunk = [&](int base, int pre) __attribute__((always_inline)) {
     const int idx = base + lane;
     len_l = idx < a.batch ? a.seq_lens[idx] : 0;
     nt_l = idx < a.batch ? seq_tiles(len_l) : 0;
-    incl_l = wave_scan_incl(nt_l, lane) + pre;
-    chunk_end = __builtin_amdgcn_readlane(incl_l, 63);
+    scan_chunk(base, pre);
   };
-  load_chunk(0, 0);
-  int all_tiles = chunk_end;
+  len_l = lane < a.batch ? a.seq_lens[lane] : 0;
+  nt_l = lane < a.batch ? seq_tiles(len_l) : 0;
+  int all_tiles = wave_sum(nt_l);
   for (int c0 = 64; c0 < a.batch; c0 += 64) {
     const int idx = c0 + lane;
     all_tiles += wave_sum(idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0);
   }
-  // tile counts fit in int32: the host bounds batch * max_pages * pages' tiles * HK
-  const int T = __builtin_amdgcn_readfirstlane(all_tiles) * hk;
+  // tile counts fit in int32: the host bounds batch * (max_pages * pages' tiles + 16) * HK
+  const int t0 = __builtin_amdgcn_readfirstlane(all_tiles) * hk;
+  lead = charged_lead(a.seq_lens, a.batch, a.waves, a.lead, nt_l, t0, lane);
+  scan_chunk(0, 0);
+  const int T = t0 + a.batch * hk * lead;
   const int W = min(a.waves, T);
   if (w >= W) return;
   Split sp;
   sp.init(T, W);
 
-  // the segment holding tile g (uniform): sequence, KV head, length, tiles, first tile
+  // the segment holding split tile g (uniform): sequence, KV head, length,
+  // tiles, and its first split tile (its tiles follow lead split tiles later)
   auto locate = [&](int gt, int &pb, int &pkh, int &pL, int &pnt, int &pseg0)
       __attribute__((always_inline)) {
     if (gt < chunk_pre * hk) load_chunk(0, 0);
@@ -314,9 +361,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     pb = cbase + f;
     pnt = __builtin_amdgcn_readlane(nt_l, f);
     pL = __builtin_amdgcn_readlane(len_l, f);
-    const int pre = (__builtin_amdgcn_readlane(incl_l, f) - pnt) * hk;
-    pkh = (gt - pre) / pnt;
-    pseg0 = pre + pkh * pnt;
+    const int span = pnt + lead;
+    const int pre = (__builtin_amdgcn_readlane(incl_l, f) - span) * hk;
+    pkh = (gt - pre) / span;
+    pseg0 = pre + pkh * span;
   };
 
   // ---- per-piece metadata, requested a piece ahead: page-id window (page
@@ -473,8 +521,9 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   int cb, ckh, cL, cnt, cseg0;
   bool cfirst = true;
   locate(sp.start(w), cb, ckh, cL, cnt, cseg0);
-  int cta = sp.start(w) - cseg0;
-  int ctb = min(cnt, run_end - cseg0);
+  int cta = max(sp.start(w) - cseg0 - lead, 0);
+  int ctb = min(cnt, run_end - cseg0 - lead);
+  if (ctb <= 0) return;  // the run holds lead tiles only: no piece
   int cpid = fetch_window(cb, cta >> tpp_shift, min(cL, ctb * PKV_TILE));
 
   bool has_next = false;
@@ -484,8 +533,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   // page-id window (read at the next switch)
   auto set_next = [&](int gstart) __attribute__((always_inline)) {
     locate(gstart, nb, nkh, nL, nnt, nseg0);
-    nta = gstart - nseg0;
-    ntb = min(nnt, run_end - nseg0);
+    nta = max(gstart - nseg0 - lead, 0);
+    ntb = min(nnt, run_end - nseg0 - lead);
     npid = fetch_window(nb, nta >> tpp_shift, min(nL, ntb * PKV_TILE));
   };
 
@@ -510,8 +559,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       load_v(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.vmeta_offset));
       set_queries(cL, width, t1, raw, qp);
       // the rest of the run is the next piece: its page-id window now
-      has_next = cseg0 + ctb < run_end;
-      if (has_next) set_next(cseg0 + ctb);
+      has_next = ctb == cnt && cseg0 + cnt + 2 * lead < run_end;
+      if (has_next) set_next(cseg0 + lead + cnt);
     }
 
     float m[RB], lsum[RB], corr[RB][NG], osum[RB][NG];
@@ -823,6 +872,15 @@ int attention_waves(const Geo &g, int rows) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64, 0) != hipSuccess) return -1;
   return max(1, cus * per_cu);
 }
+
+// The split charges each segment `lead` tiles ahead of its own, the cost of
+// starting a piece (query rows, then its first tiles, requested after the
+// previous piece's pipeline has drained and its partial is written), so that
+// a wave whose run crosses into another segment gets correspondingly fewer
+// tiles and ends with the others.  Eight tiles measured best, or within
+// noise of it, for 1, 5 and 20 rows per KV head and contexts from 64 to
+// 16K tokens (4-slot decode: about two iterations).
+int attention_lead(const Geo &, int) { return 8; }
 
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
   const AttnKernel k = select_kernel(a.g, a.rows);

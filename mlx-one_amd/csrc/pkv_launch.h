@@ -41,6 +41,7 @@ struct AttnArgs {
   const int32_t *seq_lens, *q_pos, *widths;
   float scale_log2;  // softmax scale * log2(e)
   int waves;         // work waves (grid size)
+  int lead;          // tiles of start-up cost charged ahead of each segment in the split
   float *part_acc;   // [2*waves][rows][DP]
   float *part_ml;    // [2*waves][rows][2]
   uint16_t *out;     // [B][H][Q][D]
@@ -48,7 +49,7 @@ struct AttnArgs {
 
 struct MergeArgs {
   int batch, hk, heads, nq, gqa, rows, dim, dp, float_kind;
-  int waves;  // as launched for the attention kernel
+  int waves, lead;  // as launched for the attention kernel
   const int32_t *seq_lens;
   const float *part_acc, *part_ml;
   uint16_t *out;
@@ -121,6 +122,8 @@ hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a);
 // Resident waves of the attention kernel for this layout and row count on the
 // current device (CUs x workgroups per CU); <0 on error.
 int attention_waves(const Geo &g, int rows);
+// Lead tiles the decode split charges per segment for `rows` query rows per KV head.
+int attention_lead(const Geo &g, int rows);
 // Whether the split-K decode kernel serves this many rows per KV head (else
 // launch_prefill does, with no workspace and no merge).
 bool decode_serves(const Geo &g, int rows);

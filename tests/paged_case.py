@@ -104,12 +104,24 @@ def oracle_attention(fmt, inst, positions, widths, scale, *, ref=None, use_c=Tru
 
 
 def assert_attention_close(got, want, *, max_abs=2e-2, mean_abs=1e-3):
-    """The north-star bar: bf16 outputs within 2e-2 max-abs and 1e-3 mean-abs."""
+    """The north-star bar: bf16 outputs within 2e-2 max-abs and 1e-3 mean-abs.
+
+    The oracle is rounded to bf16 as the kernel's output is; where one bf16
+    step exceeds 2e-2 (|x| >= 8: outputs of very short sequences take single
+    tokens' outlier channels), the two may also sit one step apart, as two
+    correct f32 results on either side of a rounding boundary do.
+    """
     got = np.asarray(got, np.float32)
     want = numpy_ref.bf16_round(np.asarray(want, np.float32))
     err = np.abs(got - want)
     assert np.isfinite(got).all(), "non-finite attention output"
-    assert err.max() <= max_abs, f"max abs error {err.max():.3e} > {max_abs}"
+    mag = np.maximum(np.abs(want), np.float32(1e-30))
+    step = np.exp2(np.floor(np.log2(mag)) - 7).astype(np.float32)   # one bf16 step at |want|
+    bound = np.maximum(np.float32(max_abs), step)
+    worst = int(np.argmax(err - bound))
+    assert err.flat[worst] <= bound.flat[worst], (
+        f"abs error {err.flat[worst]:.3e} > {bound.flat[worst]:.3e} at |x| = {mag.flat[worst]:.3g}"
+        f" (max abs error {err.max():.3e})")
     assert err.mean() <= mean_abs, f"mean abs error {err.mean():.3e} > {mean_abs}"
     return float(err.max()), float(err.mean())
 

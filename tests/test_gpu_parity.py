@@ -176,6 +176,13 @@ ATTN_CASES = {
                  "bfloat16", 40, 2),
     "f16_pages": (dict(name="c1", bits=16), "float16", 64, 1),
     "more_waves_than_tiles": (dict(name="c2", batch=2, lengths=(40, 3)), "bfloat16", 16, 10000),
+    # the split's lead tiles ahead of each segment: runs that end inside a
+    # lead (no piece), one-tile segments, pieces starting inside a lead
+    "lead_short_segments_waves7": (dict(name="c2", batch=6, lengths=(1, 16, 17, 300, 2, 33)),
+                                   "bfloat16", 16, 7),
+    "lead_short_segments_waves61": (dict(name="c2", batch=6, lengths=(1, 16, 17, 300, 2, 33)),
+                                    "bfloat16", 16, 61),
+    "lead_c4_waves50": (dict(name="c4", batch=3, lengths=(5, 49, 700)), "bfloat16", 64, 50),
     # few waves per (sequence, KV head): one long sequence is cut into ~40
     # pieces, the rest stay whole
     "fused_skewed_many_pieces": (dict(name="c2", batch=8, heads=4, kv_heads=1,
