@@ -183,6 +183,18 @@ ATTN_CASES = {
     "lead_short_segments_waves61": (dict(name="c2", batch=6, lengths=(1, 16, 17, 300, 2, 33)),
                                     "bfloat16", 16, 61),
     "lead_c4_waves50": (dict(name="c4", batch=3, lengths=(5, 49, 700)), "bfloat16", 64, 50),
+    # 17-32 rows per KV head (two row blocks): one metadata group per head
+    # (G128), 4-bit at 32-token pages, head_dim 64, short pieces, one wave
+    # sliding the page-id window
+    "rows17to32_c4_g128": (dict(name="c4", batch=3, length_range=(200, 700), group_size=128),
+                       "bfloat16", 64, 0),
+    "rows17to32_4bit_rows24_p32": (dict(name="c3", batch=2, lengths=(700, 1500), num_queries=3,
+                                    append_tokens=3), "bfloat16", 128, 0),
+    "rows17to32_d64_g32_waves13": (dict(name="c4", batch=3, length_range=(100, 600), head_dim=64,
+                                    group_size=32), "bfloat16", 64, 13),
+    "rows17to32_short_pieces_waves90": (dict(name="c4", batch=4, lengths=(5, 20, 37, 300)),
+                                    "bfloat16", 64, 90),
+    "rows17to32_one_wave_long": (dict(name="c4", batch=1, lengths=(2100,)), "bfloat16", 256, 1),
     # few waves per (sequence, KV head): one long sequence is cut into ~40
     # pieces, the rest stay whole
     "fused_skewed_many_pieces": (dict(name="c2", batch=8, heads=4, kv_heads=1,
