@@ -84,23 +84,30 @@ struct Conv<8> {
   }
 };
 
-__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int s) {
-  return ((w >> (4 * s)) & 0x000F000Fu) | 0x64006400u;
-}
+// 4-bit codes: f16 pair s of a word x holds nibbles s and s + 4, i.e. the
+// value ((x >> 4s) & 0x000F000F) | 0x64006400.  The even nibbles
+// (x & 0x0F0F0F0F) and the odd ones ((x >> 4) & 0x0F0F0F0F) each sit one per
+// byte, so one v_perm per pair places two of them beside the exponent byte:
+// seven instructions per word instead of eleven.
+constexpr uint32_t kNibLo = 0x00060004u;  // bytes 0 and 2 of the nibble word
+constexpr uint32_t kNibHi = 0x00070005u;  // bytes 1 and 3
 
 template <>
 struct Conv<4> {
   template <int LW>
   static __device__ __forceinline__ h8 kop(const uint32_t (&w)[LW], int kb) {
     const uint32_t x = w[kb];
-    u4 r = {nib_pair(x, 0), nib_pair(x, 1), nib_pair(x, 2), nib_pair(x, 3)};
+    const uint32_t ev = x & 0x0F0F0F0Fu, od = (x >> 4) & 0x0F0F0F0Fu;
+    u4 r = {perm(ev, kMagic, kNibLo), perm(od, kMagic, kNibLo), perm(ev, kMagic, kNibHi),
+            perm(od, kMagic, kNibHi)};
     return __builtin_bit_cast(h8, r);
   }
   template <int LW>
   static __device__ __forceinline__ h4 vop(const uint32_t (&w)[LW], int n) {
     const uint32_t x = w[n >> 1];
-    const int o = n & 1;
-    u2 r = {nib_pair(x, o), nib_pair(x, 2 + o)};
+    // pairs (0, 2) from the even nibbles, (1, 3) from the odd ones
+    const uint32_t nb = (n & 1) ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
+    u2 r = {perm(nb, kMagic, kNibLo), perm(nb, kMagic, kNibHi)};
     return __builtin_bit_cast(h4, r);
   }
 };
