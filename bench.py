@@ -8,7 +8,11 @@ sequence + paged attention of the new query over all L_b + 1 tokens.
 Steps rotate over ``--layers`` independent layer pools (default 4, ~1.3 GB of
 KV) so that a step never finds its KV in the 256 MB Infinity Cache, the same
 access pattern a 32-layer model has.  Inputs are synthetic and resident in HBM
-before timing.  Prints one JSON line (rank 0).
+before timing.  The timed steps are captured as one HIP graph and replayed
+once untimed, then once timed for the step time (``--eager`` launches them
+from the host instead); ``roofline.achieved`` comes from HIP events around
+each attention launch in a host-launched pass over the same steps
+(``roofline.kernel_timing``).  Prints one JSON line (rank 0).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
 """
@@ -409,7 +413,12 @@ def main(argv=None):
                         help="attention work waves (0: the workload's partition size, else the "
                              "library default for the shape and batch)")
     parser.add_argument("--graph", action="store_true",
-                        help="replay the timed steps as one captured HIP graph")
+                        help="layer workload: replay each decode step as a captured HIP graph "
+                             "(the attention workloads replay their timed steps as one graph "
+                             "unless --eager)")
+    parser.add_argument("--eager", action="store_true",
+                        help="attention workloads: launch each timed step from the host instead "
+                             "of replaying them as one captured HIP graph")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
                         help="seconds of CPU baseline timing (0 disables)")
     parser.add_argument("--arena", choices=("host", "device"), default="host",
@@ -466,7 +475,6 @@ def main(argv=None):
 
     lib = _native.load()
     layout = fmt.c_layout
-    stream = torch.cuda.current_stream(device)
 
     def step(s, ev=None):
         li, start, lens, _ = plans[s]
@@ -480,7 +488,7 @@ def main(argv=None):
             if code:
                 _native.check(code, "append")
         if ev is not None:
-            ev[0].record(stream)
+            ev[0].record(torch.cuda.current_stream(device))
         code = lib.pkv_paged_attention(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                        layer.queries.data_ptr(), w.batch, w.heads, w.num_queries,
                                        layer.table.data_ptr(), layer.table.shape[1],
@@ -488,7 +496,7 @@ def main(argv=None):
                                        workspace.data_ptr(), workspace.numel(),
                                        layer.out.data_ptr())
         if ev is not None:
-            ev[1].record(stream)
+            ev[1].record(torch.cuda.current_stream(device))
         if code:
             _native.check(code, "attention")
 
@@ -503,28 +511,45 @@ def main(argv=None):
         step(s)
     torch.cuda.synchronize()
 
+    # The timed steps are captured as one HIP graph and replayed (no host
+    # launch gaps): that replay gives the step time.  Events cannot be captured
+    # inside the graph on ROCm, so a host-launched pass over the same steps
+    # follows, with HIP events around each attention launch on its stream:
+    # that pass gives the launch duration for the roofline.  Re-running a step
+    # re-appends the same token at the same position (idempotent).
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps)]
-    if args.graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(args.steps):
-                step(args.warmup + i)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+    graph = None
+    if not args.eager:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(args.steps):
+                    step(args.warmup + i)
+            graph.replay()          # untimed: the first replay uploads the graph
+            torch.cuda.synchronize()
+        except RuntimeError as exc:
+            print(f"bench: graph capture unavailable ({exc}); timing host launches",
+                  file=sys.stderr)
+            graph = None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if graph is not None:
         graph.replay()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        attn_ms = None
     else:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(args.warmup + i, events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    if graph is not None:
         for i in range(args.steps):
             step(args.warmup + i, events[i])
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
     ms_per_step = wall / args.steps * 1e3
+    timing = ("HIP events per launch, host-launched pass over the timed steps after the "
+              "timed graph replay" if graph is not None else
+              "HIP events per launch in the timed host-launched steps")
     timed = plans[args.warmup:]
     mean_lens = np.mean([p[3] for p in timed], axis=0)
     attn_bytes, step_bytes = algorithmic_bytes(w, mean_lens)
@@ -538,6 +563,7 @@ def main(argv=None):
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
                     "traffic": measured_traffic(w.name),
                     "kernel": "pkv_paged_attention (prefill_kernel)",
+                    "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "flops_per_launch": int(flops),
                     "bytes_per_launch": int(attn_bytes),
                     "hbm_gbs": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1)}
@@ -547,6 +573,7 @@ def main(argv=None):
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(w.name),
                     "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
+                    "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if prefill:
         metric = "chunked-prefill attention query tok/s (int8 paged KV, 1 layer)"
@@ -564,7 +591,7 @@ def main(argv=None):
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
                    "bits": w.bits, "group_size": w.group_size, "num_queries": w.num_queries,
                    "mean_context": float(mean_lens.mean()),
-                   "waves": waves, "layers_rotated": args.layers, "graph": args.graph},
+                   "waves": waves, "layers_rotated": args.layers, "graph": graph is not None},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
     }
