@@ -183,6 +183,13 @@ ATTN_CASES = {
     "lead_short_segments_waves61": (dict(name="c2", batch=6, lengths=(1, 16, 17, 300, 2, 33)),
                                     "bfloat16", 16, 61),
     "lead_c4_waves50": (dict(name="c4", batch=3, lengths=(5, 49, 700)), "bfloat16", 64, 50),
+    # more than 64 sequences: the split walks the lengths in 64-sequence
+    # chunks (segment lookup, lead alignment test, merge)
+    "b80_short_default_waves": (dict(name="c2", batch=80, length_range=(1, 300)), "bfloat16",
+                                32, 0),
+    "b80_short_waves37": (dict(name="c2", batch=80, length_range=(1, 300)), "bfloat16", 32, 37),
+    "b130_c4_waves500": (dict(name="c4", batch=130, length_range=(5, 90),
+                              shared_prefix_pages=0), "bfloat16", 32, 500),
     # 17-32 rows per KV head (two row blocks): one metadata group per head
     # (G128), 4-bit at 32-token pages, head_dim 64, short pieces, one wave
     # sliding the page-id window
