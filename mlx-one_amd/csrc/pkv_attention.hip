@@ -625,13 +625,13 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         for (int r = 0; r < 4; ++r) {
           float v;
           if constexpr (QUANT) {
-            v = 0.0f;
 #pragma unroll
             for (int gi = 0; gi < NG; ++gi) {
               const uint32_t word = km[r * NG + gi];
               const float ks = f16_bits_to_f32(word);
               const float kbias = f16_bits_to_f32(word >> 16) - 1024.0f * ks;
-              v += ks * acc[rb][gi][r] + qs[rb][gi] * kbias;
+              const float term = ks * acc[rb][gi][r] + qs[rb][gi] * kbias;
+              v = gi == 0 ? term : v + term;  // no 0.0f + term: the add would stay (signed zero)
             }
           } else {
             v = acc[rb][0][r];
@@ -674,14 +674,27 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
       }
-      // probabilities and the P operands (per group for quantized V)
+      // probabilities and the P operands (per group for quantized V).  A
+      // masked score is -inf, so its probability is exp2(-inf) = 0 (the max
+      // is finite once any score was seen).  Tokens the piece does not hold
+      // (past its end, absent tiles) get zero value metadata, whatever their
+      // page holds, so that every masked token contributes exact zeros.
+      uint32_t vmw[C::MW];
+      if constexpr (QUANT) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool held = my_ok && tok0 + r < t1;
+#pragma unroll
+          for (int gi = 0; gi < NG; ++gi) vmw[r * NG + gi] = held ? vm[r * NG + gi] : 0u;
+        }
+      }
       VT pop[RB][NG];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         float p[4];
+        const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          p[r] = vis[rb][r] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
+        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(s[rb][r] - mref);
         lsum[rb] += (p[0] + p[1]) + (p[2] + p[3]);
         if constexpr (QUANT) {
 #pragma unroll
@@ -689,11 +702,9 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             h4 pv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const uint32_t word = vm[r * NG + gi];
-              // absent tokens contribute exact zeros whatever their metadata holds
-              const _Float16 ps = (_Float16)(p[r] * f16_bits_to_f32(word));
-              pv[r] = vis[rb][r] ? ps : (_Float16)0.0f;
-              corr[rb][gi] += vis[rb][r] ? p[r] * f16_bits_to_f32(word >> 16) : 0.0f;
+              const uint32_t word = vmw[r * NG + gi];
+              pv[r] = (_Float16)(p[r] * f16_bits_to_f32(word));
+              corr[rb][gi] += p[r] * f16_bits_to_f32(word >> 16);
               osum[rb][gi] += (float)pv[r];
             }
             pop[rb][gi] = pv;
