@@ -402,6 +402,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   // query operands and row limits of the current piece
   int lim[RB];
   KT qv[RB][KB];
+  KT qsl[SLOTS > 1 ? SLOTS : 1][KB];  // per slot: the lane's query operand in that slot's columns
   float qs[RB][NG];
   auto set_queries = [&](int pL, int pwidth, int t1, const u4 (&raw)[RB][KB], const int (&qp)[RB])
       __attribute__((always_inline)) {
@@ -450,12 +451,19 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         }
       }
     }
+    if constexpr (SLOTS > 1) {
+      // slot j's operands, masked once per piece (column slots need one row block)
+      const u4 zero = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) qsl[j][kb] = slot_l == j ? qv[0][kb] : __builtin_bit_cast(KT, zero);
+    }
   };
   // slot j's query operand: the lane's rows in slot j's columns, zero elsewhere
   auto qop = [&](int j, int rb, int kb) __attribute__((always_inline)) -> KT {
     if constexpr (SLOTS == 1) return qv[rb][kb];
-    const u4 zero = {0, 0, 0, 0};
-    return slot_l == j ? qv[rb][kb] : __builtin_bit_cast(KT, zero);
+    else return qsl[j][kb];
   };
 
   // Tiles of iteration `it` of a piece (first tile pta, ntl tiles, page window
@@ -581,14 +589,6 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     auto iterate = [&](auto more, int it) __attribute__((always_inline)) {
       constexpr bool MORE = decltype(more)::value;
       refresh_lane();
-      if constexpr (SLOTS > 1) {
-        // Keep the per-slot query selects inside the loop: hoisted, they would
-        // pin SLOTS masked copies of Q in VGPRs for the whole piece.
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb) asm volatile("" : "+v"(qv[rb][kb]));
-      }
       // S^T for the iteration's tiles (slot j -> columns of slot j)
       f4 acc[RB][NG];
 #pragma unroll
