@@ -72,6 +72,7 @@ constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
   return (bits == 8 && dp == 128 && g == 64 && rb == 1 && slots == 4) ||
                  (bits == 4 && dp == 128 && g == 32 && rb == 1 && slots == 4) ||
                  (bits == 4 && dp == 128 && g == 64 && rb == 2) ||
+                 (bits == 8 && dp == 128 && g == 64 && rb == 2) ||
                  (bits == 8 && dp == 256 && g == 128 && rb == 1)
              ? 2
              : 1;
@@ -572,6 +573,13 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     }
 
     float m[RB], lsum[RB], corr[RB][NG], osum[RB][NG];
+    // Two row blocks of quantized pages take the per-column sums over tokens
+    // on the MFMA pipe instead of the VALU: csum = sum p * bias_v (the V bias
+    // term) and osum4 = sum P' (the 1024 offset), as 16x16x16 products of the
+    // tokens' f16 biases (or ones) with p (or P'); every row of the result
+    // holds the column's sum.
+    constexpr bool MSUM = RB == 2 && QUANT;
+    f4 csum[MSUM ? RB : 1][MSUM ? NG : 1], osum4[MSUM ? RB : 1][MSUM ? NG : 1];
     f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -581,6 +589,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] = 0.0f; osum[rb][gi] = 0.0f; }
+      if constexpr (MSUM) {
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) { csum[rb][gi] = f4{0, 0, 0, 0}; osum4[rb][gi] = f4{0, 0, 0, 0}; }
+      }
     }
 
     // One iteration over SLOTS tiles; with `more`, the next iteration's tiles
@@ -674,7 +686,15 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           m[rb] = mn;
           lsum[rb] *= alpha;
 #pragma unroll
-          for (int gi = 0; gi < NG; ++gi) { corr[rb][gi] *= alpha; osum[rb][gi] *= alpha; }
+          for (int gi = 0; gi < NG; ++gi) {
+            if constexpr (MSUM) {
+              csum[rb][gi] *= alpha;
+              osum4[rb][gi] *= alpha;
+            } else {
+              corr[rb][gi] *= alpha;
+              osum[rb][gi] *= alpha;
+            }
+          }
 #pragma unroll
           for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
@@ -709,10 +729,21 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             for (int r = 0; r < 4; ++r) {
               const uint32_t word = vmw[r * NG + gi];
               pv[r] = (_Float16)(p[r] * f16_bits_to_f32(word));
-              corr[rb][gi] += p[r] * f16_bits_to_f32(word >> 16);
-              osum[rb][gi] += (float)pv[r];
+              if constexpr (!MSUM) {
+                corr[rb][gi] += p[r] * f16_bits_to_f32(word >> 16);
+                osum[rb][gi] += (float)pv[r];
+              }
             }
             pop[rb][gi] = pv;
+            if constexpr (MSUM) {
+              // A: the lane's four tokens' biases (or ones) for every row; B: p (or P')
+              const h4 bias4 = __builtin_bit_cast(
+                  h4, u2{perm(vmw[NG + gi], vmw[gi], 0x07060302u), perm(vmw[3 * NG + gi], vmw[2 * NG + gi], 0x07060302u)});
+              const h4 p16 = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+              const h4 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+              csum[rb][gi] = FO::pv(bias4, p16, csum[rb][gi]);
+              osum4[rb][gi] = FO::pv(ones, pv, osum4[rb][gi]);
+            }
           }
         } else {
           pop[rb][0] = FO::pack_p(p[0], p[1], p[2], p[3]);
@@ -768,10 +799,15 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi) {
-        corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
-        corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
-        osum[rb][gi] += __shfl_xor(osum[rb][gi], 16, 64);
-        osum[rb][gi] += __shfl_xor(osum[rb][gi], 32, 64);
+        if constexpr (MSUM) {  // already summed over the tokens of every lane
+          corr[rb][gi] = csum[rb][gi][0];
+          osum[rb][gi] = osum4[rb][gi][0];
+        } else {
+          corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
+          corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
+          osum[rb][gi] += __shfl_xor(osum[rb][gi], 16, 64);
+          osum[rb][gi] += __shfl_xor(osum[rb][gi], 32, 64);
+        }
       }
       float mrow = m[rb], lrow = lsum[rb], wgt = 1.0f;
       if constexpr (SLOTS > 1) {
