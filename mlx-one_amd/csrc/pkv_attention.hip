@@ -352,7 +352,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   sp.init(T, W);
 
   // the segment holding split tile g (uniform): sequence, KV head, length,
-  // tiles, and its first split tile (its tiles follow lead split tiles later)
+  // tiles, and its first split tile (its own tiles start `lead` split tiles later)
   auto locate = [&](int gt, int &pb, int &pkh, int &pL, int &pnt, int &pseg0)
       __attribute__((always_inline)) {
     if (gt < chunk_pre * hk) load_chunk(0, 0);
