@@ -62,6 +62,19 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
   const int kh = (int)(item % g.hk);
   const int t = (int)((item / g.hk) % a.tokens);
   const int b = (int)(item / ((int64_t)g.hk * a.tokens));
+  // The new rows first: every (sequence, token, KV head) row of the inputs
+  // exists, and they do not depend on the position and page lookups below,
+  // so both requests are in flight together.
+  const int64_t row = (((int64_t)b * g.hk + kh) * a.tokens + t) * g.dim;
+  const uint16_t *src[2] = {a.keys + row, a.values + row};
+  uint16_t raw[2][EPL];
+#pragma unroll
+  for (int side = 0; side < 2; ++side)
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int d = lane * EPL + i;
+      raw[side][i] = d < g.dim ? src[side][d] : (uint16_t)0;
+    }
   const int width = a.widths ? a.widths[b] : a.tokens;
   if (a.new_lens && t == 0 && kh == 0 && lane == 0) a.new_lens[b] = a.start_pos[b] + width;
   if (t >= width) return;
@@ -73,8 +86,6 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
   uint8_t *head = a.pool + (int64_t)page * g.page_bytes + (int64_t)kh * g.head_bytes;
   const int64_t tile = (int64_t)(slot / PKV_TILE) * g.tile_bytes;
   uint8_t *ktile = head + tile, *vtile = head + g.v_offset + tile;
-  const int64_t row = (((int64_t)b * g.hk + kh) * a.tokens + t) * g.dim;
-  const uint16_t *src[2] = {a.keys + row, a.values + row};
 
   if (BITS == 16) {
     // float pages: scatter the input bits
@@ -82,7 +93,7 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
         const int d = lane * EPL + i;
-        const uint16_t v = d < g.dim ? src[side][d] : (uint16_t)0;
+        const uint16_t v = raw[side][i];
         int64_t off;
         if (side == 0) {
           const int kb = d / 32, jj = (d % 32) / 8, e = d % 8;
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int d = lane * EPL + i;
-      x[i] = d < g.dim ? bits_to_float(src[side][d], g.float_kind) : 0.0f;  // zero pad
+      x[i] = d < g.dim ? bits_to_float(raw[side][i], g.float_kind) : 0.0f;  // zero pad
     }
     quantize_row<EPL>(x, lane, g.group, BITS, s_codes[wave][side], s_meta[wave][side]);
   }
