@@ -157,8 +157,8 @@ __device__ __forceinline__ int charged_lead(const int32_t *lens, int batch, int 
 }
 
 // Log-sum-exp merge of partition partials (paged_attention.py:191-204, in
-// the exp2 domain): one NW-wave workgroup (4, or 2 when there are so many
-// units that 4-wave groups would not all be resident) per (segment, query
+// the exp2 domain): one NW-wave workgroup (1, 2 or 4 waves, as many as a
+// segment's pieces need at 16 per wave) per (segment, query
 // row) of a segment split over several waves' runs; whole segments were
 // written by the attention kernel.  Every wave finds M = max m and
 // S = sum l 2^(m - M) over the pieces (lanes stride the pieces); wave w
@@ -169,7 +169,7 @@ template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   constexpr int PER = DP / 64 > 0 ? DP / 64 : 1;  // output columns per lane
   constexpr int KW = 16;                          // pieces per wave in flight
-  __shared__ float s_acc[NW - 1][64 * PER];
+  __shared__ float s_acc[NW > 1 ? NW - 1 : 1][64 * PER];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = blockIdx.x;
@@ -948,13 +948,19 @@ hipError_t launch_merge(hipStream_t stream, const MergeArgs &a) {
   const int64_t units = (int64_t)a.batch * a.hk * a.rows;  // one workgroup per (segment, row)
   if (units == 0 || a.waves <= 1) return hipSuccess;  // one run covers every segment whole
   if (units > 0x7FFFFFFF) return hipErrorInvalidValue;
-  // Two-wave workgroups when four-wave ones would not all be resident at once
-  // (about 8,192 waves on the device), so the merge runs in one round.
-  const bool narrow = units * 4 > kMergeResidentWaves;
-  const dim3 grid((unsigned)units), block(narrow ? 128 : 256);
+  // Waves per workgroup: enough for a segment's pieces, about waves /
+  // segments + 1, to fit one round of 16 partial rows per wave (a single wave
+  // needs no LDS reduction); two instead of four when four-wave workgroups
+  // would not all be resident at once (about 8,192 waves on the device).
+  const int64_t segments = (int64_t)a.batch * a.hk;
+  const int64_t pieces = (a.waves + segments - 1) / segments + 1;
+  int nw = pieces <= 16 ? 1 : pieces <= 32 ? 2 : 4;
+  if (nw == 4 && units * 4 > kMergeResidentWaves) nw = 2;
+  const dim3 grid((unsigned)units), block(64 * nw);
 #define PKV_M(DP_)                                                                         \
   if (a.dp == DP_) {                                                                       \
-    if (narrow) hipLaunchKernelGGL((merge_kernel<DP_, 2>), grid, block, 0, stream, a);     \
+    if (nw == 1) hipLaunchKernelGGL((merge_kernel<DP_, 1>), grid, block, 0, stream, a);    \
+    else if (nw == 2) hipLaunchKernelGGL((merge_kernel<DP_, 2>), grid, block, 0, stream, a); \
     else hipLaunchKernelGGL((merge_kernel<DP_, 4>), grid, block, 0, stream, a);            \
     return hipGetLastError();                                                              \
   }
