@@ -608,13 +608,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) acc[rb][gi] = f4{0, 0, 0, 0};
 #pragma unroll
-      // Quantized tiles run every slot's MFMAs, present or not: an absent
-      // tile reads page 0, whose codes are finite f16 operands (1024 + c), its
-      // scores are masked and its P' is zero -- no branch, and the first MFMA
-      // of each chain takes the zero accumulator directly.  Float pages skip
-      // absent tiles (stale bits there may be NaN, and NaN * 0 is NaN).
       for (int j = 0; j < SLOTS; ++j) {
-        if (QUANT || (cmask & (1 << j))) {
+        if (cmask & (1 << j)) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             KT kop;
@@ -752,7 +747,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       // O^T += V^T . P'^T for each tile
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
-        if (QUANT || (cmask & (1 << j))) {
+        if (cmask & (1 << j)) {
           VT bop[RB][NG];
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)

@@ -356,3 +356,57 @@ def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(eager, first)
 
+
+
+def _random_attention_cases(count, seed):
+    """Seeded random decode/verify cases across the decode kernel's shapes."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        bits = int(rng.choice([4, 8, 8, 16]))
+        dim = int(rng.choice([64, 128, 128, 100]))
+        group = int(rng.choice([32, 64])) if bits != 16 else 32
+        if bits != 16 and -(-dim // group) * group not in (64, 128, 256):
+            group = 32
+        page = int(rng.choice([16, 32, 64]))
+        kv_heads = int(rng.choice([1, 2, 8]))
+        gqa = int(rng.choice([1, 2, 4, 8]))
+        nq = int(rng.integers(1, 5))
+        while nq * gqa > 32:
+            nq -= 1
+        batch = int(rng.integers(1, 12))
+        lengths = tuple(int(x) for x in rng.choice([1, 2, 15, 16, 17, 31, 64, 65, 129, 300, 777],
+                                                   size=batch))
+        waves = int(rng.choice([0, 1, 3, 7, 16, 50, 200, 1000]))
+        cases.append(dict(bits=bits, head_dim=dim, group_size=group, page_tokens=page,
+                          kv_heads=kv_heads, heads=kv_heads * gqa, num_queries=nq,
+                          append_tokens=nq, batch=batch, lengths=lengths, waves=waves,
+                          seed=int(rng.integers(1 << 30)), index=i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026),
+                         ids=lambda c: f"r{c['index']}")
+def test_attention_random_shapes_match_oracle(case):
+    """Random layouts (4/8-bit G32/G64 and bf16 pages, D 64-128, pages of
+    16-64 tokens), 1-32 rows per KV head, ragged batches of 1-777 tokens and
+    1-1000 waves: the split's lead tiles, runs inside a lead, column slots,
+    two row blocks and every merge width, against the oracle."""
+    from pkv import ops, workloads
+
+    case = dict(case)
+    waves = case.pop("waves")
+    case.pop("index")
+    w = workloads.get("c2", shared_prefix_pages=0, outlier_fraction=0.0, length_range=(),
+                      **case)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    widths = np.full(w.batch, w.num_queries, np.int32)
+    scale = scale_of(w.head_dim)
+    out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
+                              scale=scale, q_pos=torch.from_numpy(inst.positions).cuda(),
+                              waves=waves)
+    torch.cuda.synchronize()
+    want = oracle_attention(fmt, inst, inst.positions, widths, scale)
+    assert_attention_close(out.float().cpu().numpy(), want)
