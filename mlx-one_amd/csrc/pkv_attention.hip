@@ -694,13 +694,13 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
       }
-      // probabilities and the P operands (per group for quantized V).  A
-      // masked score is -inf, so its probability is exp2(-inf) = 0 (the max
-      // is finite once any score was seen).  Tokens the piece does not hold
-      // (past its end, absent tiles) get zero value metadata, whatever their
-      // page holds, so that every masked token contributes exact zeros.
-      uint32_t vmw[C::MW];
-      if constexpr (QUANT) {
+      // probabilities and the P operands (per group for quantized V).  Masked
+      // tokens contribute exact zeros through selects, whatever their page
+      // holds.  The column-sum products take the tokens' biases as an MFMA
+      // operand, so for them the value metadata of tokens the piece does not
+      // hold (past its end, absent tiles) is cleared as well.
+      uint32_t vmw[MSUM ? C::MW : 1];
+      if constexpr (MSUM) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool held = my_ok && tok0 + r < t1;
@@ -712,9 +712,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         float p[4];
-        const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(s[rb][r] - mref);
+        for (int r = 0; r < 4; ++r) p[r] = vis[rb][r] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
         lsum[rb] += (p[0] + p[1]) + (p[2] + p[3]);
         if constexpr (QUANT) {
 #pragma unroll
@@ -722,10 +721,11 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             h4 pv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const uint32_t word = vmw[r * NG + gi];
-              pv[r] = (_Float16)(p[r] * f16_bits_to_f32(word));
+              const uint32_t word = vm[r * NG + gi];
+              const _Float16 ps = (_Float16)(p[r] * f16_bits_to_f32(word));
+              pv[r] = vis[rb][r] ? ps : (_Float16)0.0f;
               if constexpr (!MSUM) {
-                corr[rb][gi] += p[r] * f16_bits_to_f32(word >> 16);
+                corr[rb][gi] += vis[rb][r] ? p[r] * f16_bits_to_f32(word >> 16) : 0.0f;
                 osum[rb][gi] += (float)pv[r];
               }
             }

@@ -385,7 +385,17 @@ def _random_attention_cases(count, seed):
     return cases
 
 
-@pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026),
+# A case that once failed by one sequence (4-bit D128 G32 at 16-token pages,
+# 4 rows per KV head, sequences of 3 tokens next to longer ones) when masked
+# probabilities were taken as exp2(-inf) instead of through selects.
+_RANDOM_REGRESSIONS = [
+    dict(bits=4, head_dim=128, group_size=32, page_tokens=16, kv_heads=8, heads=16, num_queries=2,
+         append_tokens=2, batch=11, lengths=(1, 1, 129, 64, 1, 65, 17, 65, 16, 64, 17), waves=200,
+         seed=765951576, index="reg0"),
+]
+
+
+@pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026) + _RANDOM_REGRESSIONS,
                          ids=lambda c: f"r{c['index']}")
 def test_attention_random_shapes_match_oracle(case):
     """Random layouts (4/8-bit G32/G64 and bf16 pages, D 64-128, pages of
