@@ -202,19 +202,31 @@ def cpu_baseline(w, inst, layer, device, budget_s):
     step_s = float(np.median(times))
     if is_prefill(w):
         return {"value": rows * w.num_queries / step_s, "unit": "tok/s", "cores": cores,
-                "kind": "port",
+                "cpu_model": cpu_model(), "kind": "port",
                 "sample": f"{w.name} step of {rows} of {w.batch} sequences (quantize its "
                           f"{w.append_tokens} new K/V rows + causal attention of its "
                           f"{w.num_queries}-token chunk over {int(lengths[0])} tokens), median "
                           f"of {reps}, OpenMP C restatement (oracle/pkv_oracle.c) on "
                           f"reference-format pages",
                 "ms_per_step": step_s * 1e3}, want
-    return {"value": rows / step_s, "unit": "seqs*tok/s", "cores": cores, "kind": "port",
+    return {"value": rows / step_s, "unit": "seqs*tok/s", "cores": cores,
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"full {w.name} step ({rows} sequences, 1 layer: quantize the new K/V "
                       f"rows + attention over {int(lengths.sum())} cached tokens), median of "
                       f"{reps}, OpenMP C restatement (oracle/pkv_oracle.c) on "
                       f"reference-format pages",
             "ms_per_step": step_s * 1e3}, want
+
+
+def cpu_model():
+    """The host CPU's model name (``lscpu``'s "Model name", from /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def copy_probe():

@@ -601,6 +601,22 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     auto iterate = [&](auto more, int it) __attribute__((always_inline)) {
       constexpr bool MORE = decltype(more)::value;
       refresh_lane();
+      // Float pages: a page reused after another sequence may hold anything
+      // past this piece's last token, and the column-slot products multiply
+      // a slot's K rows by other slots' zero query columns (and every V row by
+      // its P), so 0 * inf would spread.  Those rows are zeroed in registers
+      // in the iteration that holds the piece's end.  (Codes are always finite.)
+      const bool tail_it = t0 + (it + 1) * SLOTS * PKV_TILE > t1;
+      if constexpr (!QUANT) {
+        if (tail_it) {
+#pragma unroll
+          for (int j = 0; j < SLOTS; ++j) {
+            const bool dead = t0 + (it * SLOTS + j) * PKV_TILE + col >= t1;
+#pragma unroll
+            for (int x = 0; x < C::LW; ++x) kw[j][x] = dead ? 0u : kw[j][x];
+          }
+        }
+      }
       // S^T for the iteration's tiles (slot j -> columns of slot j)
       f4 acc[RB][NG];
 #pragma unroll
@@ -742,6 +758,21 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           }
         } else {
           pop[rb][0] = FO::pack_p(p[0], p[1], p[2], p[3]);
+        }
+      }
+      if constexpr (!QUANT) {
+        if (tail_it) {  // V rows past the piece's end (see the K rows above)
+#pragma unroll
+          for (int j = 0; j < SLOTS; ++j) {
+            const int tb = t0 + (it * SLOTS + j) * PKV_TILE + 4 * jj;
+            const uint32_t keep01 = (tb < t1 ? 0x0000FFFFu : 0u) | (tb + 1 < t1 ? 0xFFFF0000u : 0u);
+            const uint32_t keep23 = (tb + 2 < t1 ? 0x0000FFFFu : 0u) | (tb + 3 < t1 ? 0xFFFF0000u : 0u);
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+              vw[j][2 * n] &= keep01;
+              vw[j][2 * n + 1] &= keep23;
+            }
+          }
         }
       }
       // O^T += V^T . P'^T for each tile

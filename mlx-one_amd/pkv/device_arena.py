@@ -191,17 +191,40 @@ class DevicePageArena:
         head = self.state[:2].cpu().tolist()
         return head[0], head[1]
 
+    @staticmethod
+    def _raise(err):
+        if err & (BAD_ARGUMENT | CORRUPT):
+            raise CacheCorruptionError(f"device arena error bits {err:#x}")
+        raise CacheCapacityError(
+            "device arena out of pages" if err & OUT_OF_PAGES else
+            "sequence exceeds the arena's table", retryable=bool(err & OUT_OF_PAGES))
+
     def check(self):
         """Raise the first recorded device error (and clear the record)."""
         free, err = self.status()
         if err:
             self.state[1:2].zero_()
-            if err & (BAD_ARGUMENT | CORRUPT):
-                raise CacheCorruptionError(f"device arena error bits {err:#x}")
-            raise CacheCapacityError(
-                "device arena out of pages" if err & OUT_OF_PAGES else
-                "sequence exceeds the arena's table", retryable=bool(err & OUT_OF_PAGES))
+            self._raise(err)
         return free
+
+    def error_probe(self):
+        """Enqueue a copy of the error bits (as the stream stands now) into pinned
+        host memory; ``probe_failed(probe)`` reads it once that point of the
+        stream has run -- usually long before the caller asks."""
+        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        host.copy_(self.state[1:2], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(self.device))
+        return host, event
+
+    def probe_failed(self, probe):
+        """The error bits a probe saw (0 if none); a set bit is cleared on the device."""
+        host, event = probe
+        event.synchronize()
+        err = int(host[0])
+        if err:
+            self.state[1:2].zero_()
+        return err
 
     def refcounts(self):
         return self.state[HEADER_WORDS + self.capacity:HEADER_WORDS + 2 * self.capacity].cpu()
@@ -220,8 +243,11 @@ class DeviceBatchCache:
     layer's pool and runs paged attention, with every operand already on the
     device (``PagedBatchCache.attend``, ``engine/paged.py:245-267``)."""
 
-    def __init__(self, arena, layer, reservation):
+    def __init__(self, arena, layer, reservation, *, workspace=None, waves=0):
         self.arena, self.layer, self.res = arena, layer, reservation
+        # a captured step brings its own workspace (and the waves it was sized
+        # for): the shared per-device one may be replaced by a later eager call
+        self.workspace, self.waves = workspace, waves
 
     def attend(self, queries, keys, values, *, scale, position_ids=None):
         """Queries of row b sit at positions ``starts[b] + q`` (taken before the
@@ -232,7 +258,8 @@ class DeviceBatchCache:
         ops.append_quantize(fmt, pool, keys.to(dtype).contiguous(), values.to(dtype).contiguous(),
                             self.res.table, self.res.starts, self.res.widths)
         out = ops.paged_attention(fmt, pool, queries.to(dtype).contiguous(), self.res.table,
-                                  self.res.lens, scale=scale, widths=self.res.widths)
+                                  self.res.lens, scale=scale, widths=self.res.widths,
+                                  waves=self.waves, workspace=self.workspace)
         return out.to(queries.dtype)
 
 
@@ -247,12 +274,12 @@ class DeviceRunner:
             raise ValueError("the arena needs one pool per model layer")
         self.model, self.arena = model, arena
 
-    def _forward(self, hidden, res):
+    def _forward(self, hidden, res, workspace=None, waves=0):
         batch, width, _ = hidden.shape
         positions = res.starts.view(batch, 1)
         if width > 1:
             positions = positions + torch.arange(width, dtype=torch.int32, device=hidden.device)
-        caches = tuple(DeviceBatchCache(self.arena, layer, res)
+        caches = tuple(DeviceBatchCache(self.arena, layer, res, workspace=workspace, waves=waves)
                        for layer in range(len(self.arena.pools)))
         return self.model.forward(hidden, cache=caches, position_ids=positions)
 
@@ -266,11 +293,22 @@ class DeviceRunner:
             raise ValueError("one slot and a width in 1..T per row")
         before = [self.arena.lengths[s] for s in slots]
         res = self.arena.reserve(slots, widths)
+        # the reserve kernel's error bits, read after the forward is enqueued:
+        # by then the reserve has long run, so the check costs no stall
+        probe = self.arena.error_probe()
         try:
-            return self._forward(hidden, res)
+            out = self._forward(hidden, res)
         except BaseException:
             self.arena.truncate(slots, before)
             raise
+        err = self.arena.probe_failed(probe)
+        if err:
+            # a failed reserve grew no slot (its append wrote nothing): only
+            # the host length mirror moved
+            for s, n in zip(slots, before):
+                self.arena.lengths[s] = n
+            self.arena._raise(err)
+        return out
 
     def capture_decode(self, slots, hidden):
         """A graph of one decode step (one token per slot) reading the static
@@ -281,8 +319,15 @@ class DeviceRunner:
         ``arena.sync_lengths()`` reads the device's."""
         slots_d = torch.tensor([int(s) for s in slots], dtype=torch.int32, device=self.arena.device)
         widths_d = torch.ones_like(slots_d)
+        # the graph's split-K partials live in a workspace of its own, sized
+        # for the waves fixed at capture and held by the CapturedStep
+        spec = self.model.spec
+        waves = ops.default_waves(self.arena.fmt, spec.query_heads, 1, int(slots_d.numel()))
+        workspace = torch.empty(max(256, ops.workspace_bytes(self.arena.fmt, spec.query_heads, 1,
+                                                             waves)),
+                                dtype=torch.uint8, device=self.arena.device)
         res = self.arena.reserve(slots_d, widths_d)
-        self._forward(hidden, res)
+        self._forward(hidden, res, workspace, waves)
         torch.cuda.synchronize(self.arena.device)
         graph = torch.cuda.CUDAGraph()
         stream = torch.cuda.Stream(self.arena.device)
@@ -290,10 +335,10 @@ class DeviceRunner:
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
                 res_g = self.arena.reserve(slots_d, widths_d, out=res)
-                out = self._forward(hidden, res_g)
+                out = self._forward(hidden, res_g, workspace, waves)
         torch.cuda.current_stream(self.arena.device).wait_stream(stream)
         self.arena.sync_lengths()
-        return CapturedStep(graph, out, hidden, res, (slots_d, widths_d))
+        return CapturedStep(graph, out, hidden, res, (slots_d, widths_d), workspace, waves)
 
 
 @dataclass
@@ -306,6 +351,8 @@ class CapturedStep:
     hidden: torch.Tensor            # the static input buffer
     reservation: Reservation        # the batch operands the reserve kernel rewrites
     operands: tuple                 # slot ids and widths read by the reserve kernel
+    workspace: torch.Tensor = None  # the attention's split-K partials (every layer's launch)
+    waves: int = 0                  # the attention waves the workspace is sized for
 
     def replay(self):
         self.graph.replay()

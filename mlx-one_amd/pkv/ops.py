@@ -176,9 +176,18 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
         nat.check(nat.PKV_INVALID_ARGUMENT, "paged attention workspace")
     if workspace is None:
         workspace = attention_workspace(device, need)
-    if out is None:
-        out = torch.empty_like(queries)
+    elif workspace.device != device or workspace.dtype != torch.uint8 or \
+            not workspace.is_contiguous():
+        raise ValueError("attention workspace must be a contiguous uint8 tensor on the "
+                         "queries' device")
+    # the kernels read queries and write out as dense [B, H, Q, D]
     queries = queries.contiguous()
+    if out is None:
+        out = torch.empty(queries.shape, dtype=queries.dtype, device=device)
+    elif (tuple(out.shape) != tuple(queries.shape) or out.dtype != queries.dtype
+          or out.device != device or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous tensor of the queries' shape, dtype and "
+                         "device")
     code = nat.load().pkv_paged_attention(
         nat.stream_handle(device), fmt.c_layout, nat.ptr(pool), pool.shape[0], nat.ptr(queries),
         batch, heads, nq, nat.ptr(table), table.shape[1], nat.ptr(lens),

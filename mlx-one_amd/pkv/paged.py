@@ -150,12 +150,19 @@ class PagedKVCache:
         keys, values = keys.to(dtype), values.to(dtype)
         layout = self.layout_for(keys.shape[1], keys.shape[3])
         width = int(keys.shape[2])
-        start = self._plan_append(width, layout)
-        pool = self.pool.pool_for(layout)
-        device = pool.buffer.device
-        table = torch.from_numpy(self.page_row(len(self.page_table.pages))[None]).to(device)
-        ops.append_quantize(pool.fmt, pool.buffer, keys.to(device), values.to(device), table,
-                            torch.tensor([start], dtype=torch.int32, device=device))
+        # planning takes pages one by one: a failure part way (or before the
+        # launch) must not leave the cache claiming tokens that were never written
+        mark = self.checkpoint()
+        try:
+            start = self._plan_append(width, layout)
+            pool = self.pool.pool_for(layout)
+            device = pool.buffer.device
+            table = torch.from_numpy(self.page_row(len(self.page_table.pages))[None]).to(device)
+            ops.append_quantize(pool.fmt, pool.buffer, keys.to(device), values.to(device), table,
+                                torch.tensor([start], dtype=torch.int32, device=device))
+        except BaseException:
+            self.rollback(mark)
+            raise
 
     def clone(self):
         """Branch: sealed pages are shared (refcount), the mutable tail is copied."""
@@ -285,9 +292,6 @@ class PagedBatchCache:
     def attend(self, queries, keys, values, *, scale, position_ids):
         import torch
 
-        from pkv import ops
-        from pkv.paged_attention import paged_attention
-
         batch, _, width, _ = queries.shape
         offsets = np.array([cache.offset for cache in self.rows], np.int64)
         widths = np.array(self.widths, np.int64)
@@ -300,10 +304,28 @@ class PagedBatchCache:
             given = position_ids.to("cpu", torch.int64).numpy()  # free for host tensors
             if not bool((given[mask] == positions[mask]).all()):
                 raise ValueError("paged query logical positions mismatch")
-        # host: pages for every row, then one append launch for the whole batch
+        # host: pages for every row, then one append launch for the whole batch.
+        # A failure before the launch (no free page part way through a row)
+        # rolls every row back: no row claims tokens that were never written.
         layout = self.rows[0].layout_for(keys.shape[1], keys.shape[3])
-        starts = [cache._plan_append(real, layout)
-                  for cache, real in zip(self.rows, self.widths, strict=True)]
+        marks = [cache.checkpoint() for cache in self.rows]
+        try:
+            starts = [cache._plan_append(real, layout)
+                      for cache, real in zip(self.rows, self.widths, strict=True)]
+            return self._launch(queries, keys, values, layout, starts, widths, positions,
+                                scale)
+        except BaseException:
+            for cache, mark in zip(self.rows, marks, strict=True):
+                cache.rollback(mark)
+            raise
+
+    def _launch(self, queries, keys, values, layout, starts, widths, positions, scale):
+        import torch
+
+        from pkv import ops
+        from pkv.paged_attention import paged_attention
+
+        batch, _, width, _ = queries.shape
         pool = self.rows[0].pool.pool_for(layout)
         device = pool.buffer.device
         # the step's int32 metadata in one pinned buffer and one host->device copy:

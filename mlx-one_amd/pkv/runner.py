@@ -165,7 +165,12 @@ class PagedRunner:
                 drafts = []
                 try:
                     for r in requests:
-                        drafts.append([c.clone() for c in r.cache])
+                        # listed before they are filled: a clone that fails part
+                        # way still leaves the earlier layers' clones to reset
+                        layers = []
+                        drafts.append(layers)
+                        for c in r.cache:
+                            layers.append(c.clone())
                     run(drafts)
                     # commit: the drafts become the request caches (old refs closed)
                     for r, layers in zip(requests, drafts, strict=True):

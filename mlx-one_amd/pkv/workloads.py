@@ -70,10 +70,20 @@ def get(name, **overrides):
 
 
 def bf16_round(x):
-    """float32 -> bfloat16 values (round to nearest even), kept as float32."""
+    """float32 -> bfloat16 values (round to nearest even), kept as float32.
+
+    32-bit integer arithmetic: the largest finite pattern plus the rounding
+    increment stays below 2**32; NaNs stay NaN."""
     x = np.ascontiguousarray(x, np.float32)
-    bits = x.view(np.uint32).astype(np.uint64)
-    return ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    bits = x.view(np.uint32)
+    out = bits + np.uint32(0x7FFF)
+    out += (bits >> np.uint32(16)) & np.uint32(1)
+    out &= np.uint32(0xFFFF0000)
+    out = out.view(np.float32)
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = np.float32("nan")
+    return out
 
 
 @dataclass

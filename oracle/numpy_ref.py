@@ -24,11 +24,15 @@ def bf16_round(x):
     tie-case bit patterns.  NaN inputs stay NaN.
     """
     x = np.ascontiguousarray(x, dtype=np.float32)
-    bits = x.view(np.uint32).astype(np.uint64)
-    rounded = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
-    out = rounded.astype(np.uint32).view(np.float32).copy()
+    bits = x.view(np.uint32)
+    # 32-bit arithmetic: the largest finite pattern plus the increment fits
+    rounded = bits + np.uint32(0x7FFF)
+    rounded += (bits >> np.uint32(16)) & np.uint32(1)
+    rounded &= np.uint32(0xFFFF0000)
+    out = rounded.view(np.float32)
     nan = np.isnan(x)
-    out[nan] = np.float32("nan")
+    if nan.any():
+        out[nan] = np.float32("nan")
     return out
 
 

@@ -104,26 +104,44 @@ def oracle_attention(fmt, inst, positions, widths, scale, *, ref=None, use_c=Tru
 
 
 def assert_attention_close(got, want, *, max_abs=2e-2, mean_abs=1e-3):
-    """The north-star bar: bf16 outputs within 2e-2 max-abs and 1e-3 mean-abs.
+    """``assert_attention_close_f32`` returning (max abs error, mean abs error);
+    elements over ``max_abs`` (allowed only where half a bf16 step is larger)
+    are printed."""
+    worst, mean, over = assert_attention_close_f32(got, want, max_abs=max_abs,
+                                                   mean_abs=mean_abs)
+    if over:
+        print(f"attention: {over} elements over {max_abs} (|x| >= 8), max abs {worst:.3e}")
+    return worst, mean
 
-    The oracle is rounded to bf16 as the kernel's output is; where one bf16
-    step exceeds 2e-2 (|x| >= 8: outputs of very short sequences take single
-    tokens' outlier channels), the two may also sit one step apart, as two
-    correct f32 results on either side of a rounding boundary do.
+
+def assert_attention_close_f32(got, want, *, max_abs=2e-2, mean_abs=1e-3):
+    """The north-star bar against the oracle's float32 result.
+
+    ``got`` is the kernel's bf16 output.  Max-abs is taken against the
+    unrounded result: every element is within ``max_abs`` except where half a
+    bf16 step at |want| is itself larger (|want| >= 8: rounding to bf16 alone
+    can move the value that far); there the bound is half a step plus
+    2^-9 |want| for the kernel's own arithmetic.  Mean-abs ("in bf16") is taken
+    against the result rounded to bf16: outputs of magnitude ~1 carry ~2e-3
+    of rounding error on average in bf16 whatever computes them, so against
+    the unrounded values the bar would measure the format, not the kernel.
+    Returns (max abs error, mean abs error, elements over ``max_abs``).
     """
     got = np.asarray(got, np.float32)
-    want = numpy_ref.bf16_round(np.asarray(want, np.float32))
-    err = np.abs(got - want)
+    want = np.asarray(want, np.float32)
+    assert got.shape == want.shape
     assert np.isfinite(got).all(), "non-finite attention output"
+    err = np.abs(got - want)
     mag = np.maximum(np.abs(want), np.float32(1e-30))
-    step = np.exp2(np.floor(np.log2(mag)) - 7).astype(np.float32)   # one bf16 step at |want|
-    bound = np.maximum(np.float32(max_abs), step)
+    half = np.exp2(np.floor(np.log2(mag)) - 8).astype(np.float32)   # half a bf16 step
+    bound = np.where(half > max_abs, half + mag * np.float32(2.0 ** -9), np.float32(max_abs))
     worst = int(np.argmax(err - bound))
     assert err.flat[worst] <= bound.flat[worst], (
         f"abs error {err.flat[worst]:.3e} > {bound.flat[worst]:.3e} at |x| = {mag.flat[worst]:.3g}"
         f" (max abs error {err.max():.3e})")
-    assert err.mean() <= mean_abs, f"mean abs error {err.mean():.3e} > {mean_abs}"
-    return float(err.max()), float(err.mean())
+    mean = float(np.abs(got - numpy_ref.bf16_round(want)).mean())
+    assert mean <= mean_abs, f"mean abs error {mean:.3e} > {mean_abs} (in bf16)"
+    return float(err.max()), mean, int((err > max_abs).sum())
 
 
 def scale_of(dim):

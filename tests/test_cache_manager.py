@@ -228,3 +228,91 @@ def test_prefix_reuse_rules():
     assert cm2.publish_prefix(h2, fp, tuple(range(39))) is False    # length must match
     assert fp.digest == cm2.fingerprint(key_type="q8_0", value_type="q8_0").digest
     assert fp.digest != cm2.fingerprint(key_type="q8_0", value_type="q8_0", namespace="x").digest
+
+
+# ------------------------------------------------- allocation failure sweep
+# The reference injects a failure at every page allocation of a step and
+# checks that offsets, live blocks and reserved bytes are unchanged
+# (tests/test_paged_hybrid.py:349-374).  Here the batched attend plans pages
+# for every row before its one append launch; a failure at any allocation
+# (or at the launch itself, which has no GPU to run on in this suite) must
+# roll every row back.
+
+
+def _sweep_rows(cm):
+    rows = []
+    for request_id, tokens in (("a", 20), ("b", 9)):
+        h = cm.create_handle(request_id, key_type="q8_0", value_type="q8_0")
+        cache = h.bundle.entries[0]
+        cache._plan_append(tokens, cache.layout_for(2, 64))
+        rows.append(cache)
+    return rows
+
+
+def _row_state(cache):
+    tail = cache._blocks[-1].block if cache._blocks else None
+    return (cache.offset, [r.block_id for r in cache._blocks], list(cache.page_table.pages),
+            dict(cache.page_table.entries), tail.token_count if tail else 0,
+            tail.immutable if tail else False)
+
+
+@pytest.mark.parametrize("fail_at", range(1, 6))
+def test_every_allocation_of_a_batched_attend_rolls_back(monkeypatch, fail_at):
+    from pkv.paged import PagedBatchCache
+
+    cm = _manager(block_size_tokens=16)
+    rows = _sweep_rows(cm)
+    before = [_row_state(c) for c in rows]
+    live = cm.block_pool.stats()["block_live"]
+    original, calls = cm.block_pool.allocate_ref, [0]
+
+    def allocate(*args, **kwargs):
+        calls[0] += 1
+        if calls[0] == fail_at:
+            raise MemoryError("injected page allocation")
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(cm.block_pool, "allocate_ref", allocate)
+    # 32 new tokens per row: 12 (a) / 7 (b) fill the tails, then two new pages
+    # per row -- four allocations; fail_at = 5 fails at the launch instead
+    import torch
+
+    batch = PagedBatchCache(tuple(rows), (32, 32), {})
+    q = torch.zeros((2, 8, 32, 64), dtype=torch.float16)
+    kv = torch.zeros((2, 2, 32, 64), dtype=torch.float16)
+    with pytest.raises((MemoryError, ValueError)):
+        batch.attend(q, kv, kv, scale=0.125, position_ids=None)
+    assert calls[0] == min(fail_at, 4)
+    assert [_row_state(c) for c in rows] == before
+    assert cm.block_pool.stats()["block_live"] == live
+    for cache in rows:
+        cache.page_table.validate(cache._blocks)
+    # the rows still grow normally afterwards
+    monkeypatch.setattr(cm.block_pool, "allocate_ref", original)
+    for cache in rows:
+        cache._plan_append(32, cache.layout_for(2, 64))
+    assert [c.offset for c in rows] == [52, 41]
+
+
+@pytest.mark.parametrize("fail_at", range(1, 4))
+def test_every_allocation_of_a_single_append_rolls_back(monkeypatch, fail_at):
+    cm = _manager(block_size_tokens=16)
+    cache = _sweep_rows(cm)[0]
+    before = _row_state(cache)
+    live = cm.block_pool.stats()["block_live"]
+    original, calls = cm.block_pool.allocate_ref, [0]
+
+    def allocate(*args, **kwargs):
+        calls[0] += 1
+        if calls[0] == fail_at:
+            raise MemoryError("injected page allocation")
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(cm.block_pool, "allocate_ref", allocate)
+    import torch
+
+    k = torch.zeros((1, 2, 40, 64), dtype=torch.float16)   # 12 + 16 + 12: two new pages
+    with pytest.raises((MemoryError, ValueError)):
+        cache.append(k, k)
+    assert _row_state(cache) == before
+    assert cm.block_pool.stats()["block_live"] == live

@@ -334,7 +334,18 @@ def test_device_runner_matches_the_host_runner_and_rolls_back():
     out = step.out
     host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm, handle=h)
                   for b, h in enumerate(handles)])     # the host runner takes the same step
+    # the graph's split-K partials live in a workspace the step holds: dropping
+    # and refilling the shared per-device workspace must not reach the replays
+    from pkv import ops
+
+    assert step.workspace is not None and step.waves > 0
+    assert all(step.workspace is not ws for ws in ops._WORKSPACES.values())
+    junk = []
     for i in range(3):
+        if i == 1:
+            ops._WORKSPACES.clear()
+            ops.attention_workspace(torch.device("cuda"), 32 << 20).fill_(255)
+            junk.append(torch.full((8 << 20,), -1.0, device="cuda"))
         x.copy_(torch.randn((3, 1, 256), generator=gen, device="cuda").half())
         step.replay()
         ref = host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm,

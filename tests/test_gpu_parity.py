@@ -265,6 +265,87 @@ def test_attention_matches_oracle(case):
     assert_attention_close(out.float().cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("nq", [5, 64])
+def test_attention_takes_transposed_query_views(nq):
+    """Queries laid out [B, Q, H, D] and passed as their [B, H, Q, D] transpose
+    (a strided view) give the oracle's result; a wrong-shaped or strided
+    ``out`` is rejected."""
+    from pkv import ops, workloads
+
+    w = workloads.get("c4", batch=3, length_range=(100, 400), num_queries=nq,
+                      append_tokens=nq, shared_prefix_pages=0)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    scale = scale_of(w.head_dim)
+    bqhd = to_torch(inst.queries.transpose(0, 2, 1, 3), fmt.dtype)      # [B, Q, H, D]
+    q = bqhd.transpose(1, 2)
+    assert not q.is_contiguous()
+    q_pos = torch.from_numpy(inst.positions).cuda()
+    out = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos)
+    torch.cuda.synchronize()
+    assert out.is_contiguous() and tuple(out.shape) == tuple(q.shape)
+    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, nq, np.int32), scale)
+    assert_attention_close(out.float().cpu().numpy(), want)
+    for bad in (torch.empty_like(bqhd).transpose(1, 2),                  # strided
+                torch.empty(q.shape, dtype=torch.float16, device="cuda"),  # dtype
+                torch.empty((w.batch, w.heads, nq + 1, w.head_dim), dtype=fmt.dtype,
+                            device="cuda")):                             # shape
+        with pytest.raises(ValueError, match="out must be"):
+            ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos, out=bad)
+
+
+@pytest.mark.parametrize("bits,nq,dtype", [(16, 1, "bfloat16"), (16, 5, "bfloat16"),
+                                           (16, 2, "float16"), (8, 1, "bfloat16"),
+                                           (4, 3, "bfloat16")])
+def test_attention_ignores_stale_bytes_of_reused_pages(bits, nq, dtype):
+    """Pages handed out again still hold their last owner's bytes past the new
+    sequence's end; here every byte starts as 0xFF (NaN for float pages,
+    NaN/-inf-like scales and biases for quantized ones).  Tokens past each
+    sequence's end must not reach the output."""
+    from pkv import workloads
+
+    w = workloads.get("c2", batch=5, lengths=(1, 7, 16, 33, 250), heads=16, kv_heads=4,
+                      bits=bits, num_queries=nq, append_tokens=nq, outlier_fraction=0.0,
+                      group_size=64 if bits != 16 else 32)
+    inst = workloads.generate(w)
+    if dtype == "float16":
+        inst.keys = [k.astype(np.float16).astype(np.float32) for k in inst.keys]
+        inst.values = [v.astype(np.float16).astype(np.float32) for v in inst.values]
+        inst.queries = inst.queries.astype(np.float16).astype(np.float32)
+    fmt = _fmt(w, getattr(torch, dtype))
+    from pkv import ops
+
+    stale = ops.allocate_pool(fmt, inst.num_pages).fill_(0xFF)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=16)
+    # move the written tokens onto the stale pool: copy only what fill_pages wrote
+    # by appending again into the 0xFF pool
+    lengths_h = np.array([k.shape[1] for k in inst.keys])
+    for start in range(0, int(lengths_h.max()), 16):
+        width = np.clip(lengths_h - start, 0, 16).astype(np.int32)
+        k = np.zeros((w.batch, w.kv_heads, 16, w.head_dim), np.float32)
+        v = np.zeros_like(k)
+        for b in range(w.batch):
+            n = int(width[b])
+            k[b, :, :n] = inst.keys[b][:, start:start + n]
+            v[b, :, :n] = inst.values[b][:, start:start + n]
+        ops.append_quantize(fmt, stale, to_torch(k, fmt.dtype), to_torch(v, fmt.dtype), table,
+                            torch.full((w.batch,), start, dtype=torch.int32, device="cuda"),
+                            torch.from_numpy(width).cuda())
+    scale = scale_of(w.head_dim)
+    q = to_torch(inst.queries, fmt.dtype)
+    q_pos = torch.from_numpy(inst.positions).cuda()
+    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, nq, np.int32), scale)
+    for waves in (0, 3):
+        out = ops.paged_attention(fmt, stale, q, table, lengths, scale=scale, q_pos=q_pos,
+                                  waves=waves)
+        clean = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
+                                    waves=waves)
+        torch.cuda.synchronize()
+        assert torch.equal(out, clean), waves
+        assert_attention_close(out.float().cpu().numpy(), want)
+
+
 def test_attention_padded_query_rows_are_zero():
     from pkv import ops, workloads
 

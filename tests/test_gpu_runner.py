@@ -291,3 +291,116 @@ def test_snapshot_restore_gives_the_same_steps(tmp_path):
         out_b = runner.execute([ForwardRequest("b", x, b.bundle.entries, runtime=cm2, handle=b)])
         torch.cuda.synchronize()
         assert torch.equal(out_a.logits[0], out_b.logits[0])
+
+
+@pytest.mark.parametrize("copy_on_write", [False, True])
+def test_every_page_allocation_of_a_step_rolls_back(copy_on_write, monkeypatch):
+    """The reference's allocation sweep (tests/test_paged_hybrid.py:349-374): a
+    request with a few cached tokens takes a 32-token step through a 3-layer
+    stack; a failure injected at each page allocation of the step in turn
+    leaves offsets, live blocks, page tables and reservations unchanged, and
+    the next step equals the same step on a manager that never failed."""
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=3,
+                     dtype="float16")
+    model = AttentionStack(spec, seed=8)
+    config = CacheConfig(block_size_tokens=16, key_type="q8_0", value_type="q8_0",
+                         memory_budget_bytes=1 << 30)
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    first = torch.randn((2, 256), generator=gen, device="cuda").half()
+    step = torch.randn((32, 256), generator=gen, device="cuda").half()
+    nxt = torch.randn((1, 256), generator=gen, device="cuda").half()
+    runner = PagedRunner(model, copy_on_write=copy_on_write)
+
+    def fresh():
+        cm = CacheManager(model, config)
+        h = cm.create_handle("r", key_type="q8_0", value_type="q8_0")
+        runner.execute([ForwardRequest("r", first, h.bundle.entries, phase="prefill",
+                                       runtime=cm, handle=h)])
+        return cm, h
+
+    def run(cm, h, x):
+        return runner.execute([ForwardRequest("r", x, h.bundle.entries, phase="prefill",
+                                              runtime=cm, handle=h, return_all_logits=True)])
+
+    # the untouched twin, and the number of allocations the step makes
+    cm0, h0 = fresh()
+    calls = [0]
+    original = cm0.block_pool.allocate_ref
+
+    def counting(*a, **k):
+        calls[0] += 1
+        return original(*a, **k)
+
+    monkeypatch.setattr(cm0.block_pool, "allocate_ref", counting)
+    run(cm0, h0, step)
+    monkeypatch.undo()
+    total = calls[0]
+    assert total == (9 if copy_on_write else 6)     # clones' tails + two new pages per layer
+    want = run(cm0, h0, nxt).logits[0]
+    for fail_at in range(1, total + 1):
+        cm, h = fresh()
+        state = [(c.offset, [r.block_id for r in c._blocks], list(c.page_table.pages))
+                 for c in h.bundle.entries]
+        live = cm.block_pool.stats()["block_live"]
+        count, base = [0], cm.block_pool.allocate_ref
+
+        def failing(*a, **k):
+            count[0] += 1
+            if count[0] == fail_at:
+                raise MemoryError("injected page allocation")
+            return base(*a, **k)
+
+        cm.block_pool.allocate_ref = failing
+        with pytest.raises(MemoryError, match="allocation"):
+            run(cm, h, step)
+        cm.block_pool.allocate_ref = base
+        assert [(c.offset, [r.block_id for r in c._blocks], list(c.page_table.pages))
+                for c in h.bundle.entries] == state, fail_at
+        assert cm.block_pool.stats()["block_live"] == live
+        assert h.token_count == 2
+        stats = cm.stats()
+        assert stats.reserved_bytes == 0 and stats.transient_bytes == 0
+        run(cm, h, step)
+        got = run(cm, h, nxt).logits[0]
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), fail_at
+
+
+def test_device_runner_out_of_pages_at_every_point_changes_nothing():
+    """The device arena's counterpart: a step needing N new pages with only
+    k - 1 free (k = 1..N) sets the out-of-pages bit, ``execute`` raises
+    CacheCapacityError, and lengths (device and host mirror), tables,
+    reference counts and the free stack stay as they were."""
+    from pkv.cache_errors import CacheCapacityError
+    from pkv.device_arena import DevicePageArena, DeviceRunner
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.ops import PageFormat
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, device="cuda", seed=4)
+    fmt = PageFormat(2, 64, 16, 8, 32, torch.float16)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    x0 = torch.randn((2, 20, 256), generator=gen, device="cuda").half()
+    x1 = torch.randn((2, 40, 256), generator=gen, device="cuda").half()
+    # after the 20-token prefill each slot holds 2 pages; 40 more tokens need
+    # 2 more pages per slot: N = 4
+    for free in range(0, 4):
+        arena = DevicePageArena(fmt, 4 + free, num_layers=2, max_slots=2, max_tokens=256)
+        runner = DeviceRunner(model, arena)
+        slots = [arena.open_slot() for _ in range(2)]
+        runner.execute(slots, x0)
+        assert arena.check() == free
+        lens, table = arena.lens.clone(), arena.table.clone()
+        refs, stack = arena.refcounts(), arena.free_stack()
+        mirror = list(arena.lengths)
+        with pytest.raises(CacheCapacityError):
+            runner.execute(slots, x1)
+        assert arena.check() == free                   # the error bit was taken and cleared
+        assert arena.lengths == mirror
+        assert torch.equal(arena.lens, lens) and torch.equal(arena.table, table)
+        assert torch.equal(arena.refcounts(), refs) and torch.equal(arena.free_stack(), stack)
