@@ -10,7 +10,8 @@
  * Conventions
  *  - All pointers except `layout` are device pointers (HBM) unless noted; sizes
  *    are element counts.  No entry point allocates device memory: the caller
- *    owns every buffer, including the attention workspace.
+ *    owns every buffer, including the attention workspace (the one library-held
+ *    buffer is pkv_paged_attention_noalloc's fixed scratch array, below).
  *  - `stream` is a hipStream_t passed as void* (NULL = default stream).  Work
  *    is enqueued asynchronously; entry points never synchronise.
  *  - Return value: PKV_OK or an error code; pkv_last_error() gives the text of
@@ -118,6 +119,29 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
                         int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
                         const int32_t *widths, float scale, int32_t waves, void *workspace,
                         int64_t workspace_bytes, void *out);
+
+/*
+ * pkv_paged_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (its
+ * Metal path allocates per partition).  The split-K partials live in a fixed
+ * 32 MiB device array of the library, one per GPU, held until the process
+ * ends; this entry point allocates nothing.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams, concurrent
+ * graph replays) race: order them.  No part of the array needs clearing --
+ * each launch writes every partial it reads.  waves <= 0 picks
+ * pkv_attention_default_waves, lowered to what the array holds partials for;
+ * an explicit `waves` whose partials exceed it is refused with
+ * PKV_OUT_OF_MEMORY.  The first call on a device looks up the array's device
+ * address (hipGetSymbolAddress); make it outside graph capture.  Query blocks
+ * served by the prefill kernel need no scratch.  Arguments and results are
+ * pkv_paged_attention's.
+ */
+int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const void *pool,
+                                int64_t num_pages, const void *queries, int32_t batch,
+                                int32_t num_heads, int32_t num_queries, const int32_t *block_table,
+                                int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
+                                const int32_t *widths, float scale, int32_t waves, void *out);
 
 /* Waves the attention kernel keeps resident on the current device for this
  * layout and (num_heads, num_queries) (1 for query blocks served by the

@@ -172,11 +172,18 @@ int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_head
   return workspace_parts(g, rows, waves).total;
 }
 
-int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
-                        const void *queries, int32_t batch, int32_t num_heads, int32_t num_queries,
-                        const int32_t *block_table, int32_t max_pages, const int32_t *seq_lens,
-                        const int32_t *q_pos, const int32_t *widths, float scale, int32_t waves,
-                        void *workspace, int64_t workspace_bytes, void *out) {
+}  // extern "C"
+
+namespace {
+
+// The attention entry points' common body.  `fit_waves`: when the caller
+// leaves the waves to the library, use no more than the workspace holds
+// partials for (the split is correct at any wave count).
+int paged_attention_impl(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
+                         const void *queries, int32_t batch, int32_t num_heads, int32_t num_queries,
+                         const int32_t *block_table, int32_t max_pages, const int32_t *seq_lens,
+                         const int32_t *q_pos, const int32_t *widths, float scale, int32_t waves,
+                         void *workspace, int64_t workspace_bytes, void *out, bool fit_waves) {
   pkv_geometry geo;
   if (int rc = geometry(layout, &geo)) return rc;
   if (batch < 0) return fail(PKV_INVALID_ARGUMENT, "negative batch");
@@ -228,6 +235,11 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   if (waves <= 0) {
     waves = pkv_attention_default_waves(layout, num_heads, num_queries, batch);
     if (waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
+    if (fit_waves) {
+      while (waves > 1 && workspace_parts(geo, rows, waves).total > workspace_bytes)
+        waves = std::max<int64_t>(1, std::min<int64_t>(waves - 1,
+            (int64_t)waves * workspace_bytes / workspace_parts(geo, rows, waves).total));
+    }
   }
   if (waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
   const WorkspaceParts parts = workspace_parts(geo, rows, waves);
@@ -274,6 +286,79 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   m.part_ml = a.part_ml;
   m.out = (uint16_t *)out;
   return check_launch(pkv::launch_merge((hipStream_t)stream, m), "merge launch");
+}
+
+// ---- the allocation-free attention entry point ------------------------------------
+
+// Split-K partials of pkv_paged_attention_noalloc: a fixed device array, one
+// per GPU, held until the process ends.  Host code never uses its name as an
+// address: the device address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kNoAllocScratchBytes = 32ll << 20;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The device address of this GPU's `scratch` (the current device), looked up on
+// the first call on that device; NULL with the error text set on failure.
+void *scratch_on_current_device() {
+  static std::mutex mu;
+  static void *ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(PKV_LAUNCH_FAILED, "no current HIP device (or more than 64 devices)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(PKV_LAUNCH_FAILED, std::string("scratch symbol lookup: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
+                        const void *queries, int32_t batch, int32_t num_heads, int32_t num_queries,
+                        const int32_t *block_table, int32_t max_pages, const int32_t *seq_lens,
+                        const int32_t *q_pos, const int32_t *widths, float scale, int32_t waves,
+                        void *workspace, int64_t workspace_bytes, void *out) {
+  return paged_attention_impl(stream, layout, pool, num_pages, queries, batch, num_heads,
+                              num_queries, block_table, max_pages, seq_lens, q_pos, widths, scale,
+                              waves, workspace, workspace_bytes, out, false);
+}
+
+int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const void *pool,
+                                int64_t num_pages, const void *queries, int32_t batch,
+                                int32_t num_heads, int32_t num_queries, const int32_t *block_table,
+                                int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
+                                const int32_t *widths, float scale, int32_t waves, void *out) {
+  if (waves > 0) {
+    pkv_geometry geo;
+    if (int rc = geometry(layout, &geo)) return rc;
+    const int64_t need = pkv_attention_workspace_bytes(layout, num_heads, num_queries, waves);
+    if (need > kNoAllocScratchBytes)
+      return fail(PKV_OUT_OF_MEMORY,
+                  "pkv_paged_attention_noalloc: " + std::to_string(waves) + " waves need " +
+                      std::to_string(need) + " bytes of split-K scratch, more than its fixed " +
+                      std::to_string(kNoAllocScratchBytes) + " (pass fewer waves, or 0)");
+  }
+  void *ws = scratch_on_current_device();
+  if (!ws) return PKV_LAUNCH_FAILED;
+  return paged_attention_impl(stream, layout, pool, num_pages, queries, batch, num_heads,
+                              num_queries, block_table, max_pages, seq_lens, q_pos, widths, scale,
+                              waves, ws, kNoAllocScratchBytes, out, true);
 }
 
 int pkv_gather_pages(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
