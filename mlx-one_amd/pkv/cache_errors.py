@@ -1,12 +1,18 @@
-"""Cache runtime failures, as in the reference (src/mlx_one/engine/cache_errors.py:1-37)."""
+"""Exceptions of the paged cache runtime.
+
+The class names and their bases are the reference's
+(src/mlx_one/engine/cache_errors.py:1-37): callers at the drop-in boundary
+catch them by name, and a full arena is also a ``MemoryError``.
+"""
 
 
 class CacheError(RuntimeError):
-    """Base class for cache-runtime failures."""
+    """Root of every error raised by the cache runtime."""
 
 
 class CacheCapacityError(CacheError, MemoryError):
-    """The configured cache budget cannot satisfy an allocation."""
+    """No room under the cache's byte budget (or in its page arena);
+    ``retryable`` says whether freeing memory can make the call succeed."""
 
     def __init__(self, message: str, *, retryable: bool = True) -> None:
         super().__init__(message)
@@ -14,16 +20,17 @@ class CacheCapacityError(CacheError, MemoryError):
 
 
 class CacheTopologyUnsupported(CacheError):
-    """The cache plan cannot serve the requested layer topology."""
+    """The model's layer layout is one this cache cannot hold."""
 
 
 class PrefixReuseUnsupported(CacheError):
-    """Cached prefixes cannot be reused for this request."""
+    """The request cannot take pages from the shared prefix store."""
 
 
 class KVQuantizationUnsupported(CacheError):
-    """A requested KV quantization/backend combination is unsupported."""
+    """The requested key/value precision or its pairing is not offered."""
 
 
 class CacheCorruptionError(CacheError):
-    """Internal block or reference metadata is inconsistent."""
+    """Page ownership records disagree (unknown, freed or foreign ids,
+    negative counts)."""

@@ -146,14 +146,47 @@ def test_cold_tier_budget_and_corruption(tmp_path):
         cm.publish_prefix(h, fp, tuple(range(n * 100, n * 100 + 20 + n)))
         cm.release(h)
     store = cm.cold_prefix
-    assert store.stats()["entries"] == 2                 # the oldest left
-    assert len([p for p in tmp_path.iterdir() if p.is_dir()]) == 2
+    assert store.stats()["entries"] == 2 and store.stats()["evictions"] == 1   # the oldest left
+    assert len(list(tmp_path.glob("*.pkvc"))) == 2
     assert store.preview(fp, tuple(range(0, 21)) + (9,)) == 0
     assert store.preview(fp, tuple(range(200, 222)) + (9,)) == 16
-    index = json.loads((tmp_path / "index.json").read_text())
-    gen = tmp_path / index["entries"][-1]["generation"]
-    (gen / "state.json").write_text((gen / "state.json").read_text() + " ")
+    # a flipped payload byte is caught before any page is taken
+    newest = max(tmp_path.glob("*.pkvc"), key=lambda p: p.stat().st_mtime)
+    raw = bytearray(newest.read_bytes())
+    raw[-1] ^= 0xFF
+    newest.write_bytes(bytes(raw))
+    live = cm.block_pool.stats()["block_live"]
     with pytest.raises(ValueError, match="checksum"):
         store.lookup(fp, tuple(range(200, 222)) + (9,), cm.layer_specs, page_pool=cm.block_pool)
+    assert cm.block_pool.stats()["block_live"] == live
+    # a reopened store rebuilds its catalog from the entries' headers
+    again = _cold_manager(tmp_path, ssd_max_entries=2).cold_prefix
+    assert again.stats()["entries"] == 2
+    assert again.preview(fp, tuple(range(100, 121)) + (9,)) == 16
     store.clear()
-    assert store.stats()["entries"] == 0 and not [p for p in tmp_path.iterdir() if p.is_dir()]
+    assert store.stats()["entries"] == 0 and not list(tmp_path.glob("*.pkvc"))
+
+
+def test_cold_tier_refuses_foreign_directories_and_replaces_extended_entries(tmp_path):
+    (tmp_path / "notes.txt").write_text("not a cache")
+    with pytest.raises(ValueError, match="not empty"):
+        _cold_manager(tmp_path)
+    root = tmp_path / "cold"
+    cm = _cold_manager(root)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(1000, 1070))
+    short = _filled(cm, 33, seed=1)
+    assert cm.cold_prefix.put(fp, prompt[:33], short.bundle, page_tokens=16)
+    assert not cm.cold_prefix.put(fp, prompt[:33], short.bundle, page_tokens=16)  # held already
+    long = _filled(cm, 70, seed=1)
+    assert cm.cold_prefix.put(fp, prompt, long.bundle, page_tokens=16)
+    assert cm.cold_prefix.stats()["entries"] == 1        # the 2-page entry was extended
+    assert cm.cold_prefix.preview(fp, prompt + (5,)) == 64
+    assert cm.cold_prefix.preview(fp, prompt[:20] + (5, 6, 7)) == 16
+    assert cm.cold_prefix.preview(fp, prompt[:16]) == 0  # never the last token
+    cancelled = _filled(cm, 40, seed=2)
+    assert not cm.cold_prefix.put(fp, tuple(range(40)), cancelled.bundle, page_tokens=16,
+                                  cancelled=lambda: True)
+    (root / "stray.bin").write_bytes(b"x")
+    with pytest.raises(ValueError, match="foreign"):
+        _cold_manager(root)
