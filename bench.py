@@ -69,7 +69,7 @@ def algorithmic_bytes(w, lengths):
     qo = w.batch * w.heads * w.num_queries * w.head_dim * 2 * 2
     table = 4 * sum(math.ceil(x / w.page_tokens) for x in lengths)
     attention = kv + qo + table
-    new_rows = w.batch * w.append_tokens * 2 * w.kv_heads * w.head_dim * 2
+    new_rows = float(w.step_appends().sum()) * 2 * w.kv_heads * w.head_dim * 2
     return attention, attention + new_rows
 
 
@@ -78,13 +78,29 @@ def is_prefill(w):
     return w.num_queries * (w.heads // w.kv_heads) > 32
 
 
-def attention_flops(w, lengths):
+def attention_flops(w, lengths, widths=None):
     """Causal-exact flops of one attention launch: 4*D per (query row, visible
     token) for QK^T and PV.  Query q of a chunk of Q sits at L - Q + q and sees
-    L - Q + q + 1 tokens, so a sequence costs 4*D*H*(Q*(L - Q) + Q*(Q + 1)/2)."""
-    q = w.num_queries
-    pairs = sum(q * (int(x) - q) + q * (q + 1) // 2 for x in lengths)
+    L - Q + q + 1 tokens, so a sequence costs 4*D*H*(Q*(L - Q) + Q*(Q + 1)/2)
+    (Q = the sequence's width in a mixed batch)."""
+    widths = [w.num_queries] * len(lengths) if widths is None else widths
+    pairs = sum(q * (int(x) - q) + q * (q + 1) // 2 for x, q in zip(lengths, widths))
     return 4.0 * w.head_dim * w.heads * pairs
+
+
+def mixed_roofline(w, lengths):
+    """A mixed batch's two bounds: the decode rows' algorithmic bytes (KV, Q/O,
+    block table) at the HBM peak and the prefill rows' flops at the MFMA peak;
+    ``ideal_ms`` is their sum, a lower bound for the launch."""
+    widths = [int(x) for x in w.step_widths()]
+    small = [i for i, q in enumerate(widths) if q * (w.heads // w.kv_heads) <= 32]
+    large = [i for i in range(len(widths)) if i not in small]
+    dec_bytes = kv_bytes_per_token(w) * sum(float(lengths[i]) for i in small) + len(small) * (
+        w.heads * w.head_dim * 2 * 2) + 4 * sum(math.ceil(lengths[i] / w.page_tokens)
+                                                for i in small)
+    flops = attention_flops(w, [lengths[i] for i in large], [widths[i] for i in large])
+    ideal_ms = (dec_bytes / (HBM_PEAK_GBS * 1e9) + flops / (MFMA_PEAK_TFLOPS * 1e12)) * 1e3
+    return dec_bytes, flops, ideal_ms
 
 
 class Layer:
@@ -130,6 +146,8 @@ class Layer:
                                  generator=gen, device=device).to(fmt.dtype)
         self.queries = torch.from_numpy(inst.queries).to(device=device, dtype=fmt.dtype)
         self.out = torch.empty_like(self.queries)
+        self.widths = (torch.from_numpy(w.step_widths().astype(np.int32)).to(device)
+                       if w.widths else None)
 
 
 def cpu_baseline(w, inst, layer, device, budget_s):
@@ -158,9 +176,9 @@ def cpu_baseline(w, inst, layer, device, budget_s):
         full = np.zeros((num,) + a.shape[1:], a.dtype)
         full[used] = a
         host.append(full)
-    lengths = inst.context + w.append_tokens
-    positions = (lengths[:, None] - w.num_queries + np.arange(w.num_queries)[None]).astype(np.int32)
-    widths = np.full(w.batch, w.num_queries, np.int32)
+    lengths = inst.total_lengths
+    positions = inst.positions
+    widths = inst.widths
     q = layer.queries.float().cpu().numpy()
     scale = 1.0 / math.sqrt(w.head_dim)
 
@@ -182,7 +200,7 @@ def cpu_baseline(w, inst, layer, device, budget_s):
                                      bits=w.bits, group_size=w.group_size, pages=host,
                                      scale=scale, threads=cores)
 
-    if is_prefill(w):
+    if is_prefill(w) and not w.widths:
         # a bounded sample: the first sequence's whole chunk
         rows = 1
         started = time.perf_counter()
@@ -200,6 +218,14 @@ def cpu_baseline(w, inst, layer, device, budget_s):
         run(rows)
         times.append(time.perf_counter() - t0)
     step_s = float(np.median(times))
+    if w.widths:
+        return {"value": float(widths[:rows].sum()) / step_s, "unit": "tok/s", "cores": cores,
+                "cpu_model": cpu_model(), "kind": "port",
+                "sample": f"full {w.name} step ({rows} sequences of widths "
+                          f"{sorted(set(int(x) for x in widths))}: quantize the new K/V rows + "
+                          f"causal attention over {int(lengths.sum())} tokens), median of {reps}, "
+                          f"OpenMP C restatement (oracle/pkv_oracle.c) on reference-format pages",
+                "ms_per_step": step_s * 1e3}, want
     if is_prefill(w):
         return {"value": rows * w.num_queries / step_s, "unit": "tok/s", "cores": cores,
                 "cpu_model": cpu_model(), "kind": "port",
@@ -471,14 +497,15 @@ def main(argv=None):
 
     context = inst.context.astype(np.int64)
     scale = 1.0 / math.sqrt(w.head_dim)
-    waves = args.waves or workload_waves(w, context + w.append_tokens) or ops.default_waves(
-        fmt, w.heads, w.num_queries, w.batch)
+    appends = w.step_appends()
+    waves = args.waves or workload_waves(w, context + appends) or ops.default_waves(
+        fmt, w.heads, ops.decode_queries(fmt, w.heads, w.num_queries) or w.num_queries, w.batch)
     # per-step device arrays (no host->device copies inside the timed loop)
     plans = []
     for s in range(total_steps):
         li = s % args.layers
-        start = context + (0 if w.fixed_chunk else (s // args.layers) * w.append_tokens)
-        lens = start + w.append_tokens
+        start = context + (0 if w.fixed_chunk else (s // args.layers) * appends)
+        lens = start + appends
         plans.append((li, torch.from_numpy(start.astype(np.int32)).to(device),
                       torch.from_numpy(lens.astype(np.int32)).to(device),
                       [int(x) for x in lens]))
@@ -496,7 +523,8 @@ def main(argv=None):
             code = lib.pkv_append_quantize(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                            layer.new_k.data_ptr(), layer.new_v.data_ptr(), w.batch,
                                            w.append_tokens, layer.table.data_ptr(),
-                                           layer.table.shape[1], start.data_ptr(), None, None)
+                                           layer.table.shape[1], start.data_ptr(),
+                                           _native.ptr(layer.widths), None)
             if code:
                 _native.check(code, "append")
         if ev is not None:
@@ -504,7 +532,8 @@ def main(argv=None):
         code = lib.pkv_paged_attention(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                        layer.queries.data_ptr(), w.batch, w.heads, w.num_queries,
                                        layer.table.data_ptr(), layer.table.shape[1],
-                                       lens.data_ptr(), None, None, scale, waves,
+                                       lens.data_ptr(), None, _native.ptr(layer.widths), scale,
+                                       waves,
                                        workspace.data_ptr(), workspace.numel(),
                                        layer.out.data_ptr())
         if ev is not None:
@@ -566,9 +595,19 @@ def main(argv=None):
     mean_lens = np.mean([p[3] for p in timed], axis=0)
     attn_bytes, step_bytes = algorithmic_bytes(w, mean_lens)
     prefill = is_prefill(w)
-    value = w.batch * (w.num_queries if prefill else 1) / (ms_per_step / 1e3)
+    value = float(w.step_widths().sum() if prefill else w.batch) / (ms_per_step / 1e3)
     roofline = None
-    if attn_ms and prefill:
+    if attn_ms and w.widths:
+        # decode rows on the HBM roofline, prefill rows on the MFMA one
+        dec_bytes, flops, ideal_ms = mixed_roofline(w, mean_lens)
+        roofline = {"bound": "hbm+mfma", "achieved": round(ideal_ms / attn_ms, 4), "peak": 1.0,
+                    "unit": "ideal time / launch time", "frac": round(ideal_ms / attn_ms, 4),
+                    "traffic": measured_traffic(w.name),
+                    "kernel": "pkv_paged_attention (prefill_kernel + attn_kernel + merge_kernel)",
+                    "kernel_timing": timing, "kernel_ms": round(attn_ms, 5),
+                    "ideal_ms": round(ideal_ms, 5), "decode_bytes": int(dec_bytes),
+                    "prefill_flops": int(flops)}
+    elif attn_ms and prefill:
         flops = attention_flops(w, mean_lens)
         achieved = flops / (attn_ms / 1e3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS,
@@ -587,7 +626,10 @@ def main(argv=None):
                     "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
-    if prefill:
+    if w.widths:
+        metric = "mixed decode + prefill attention query tok/s (int8 paged KV, 1 layer)"
+        unit = "tok/s"
+    elif prefill:
         metric = "chunked-prefill attention query tok/s (int8 paged KV, 1 layer)"
         unit = "tok/s"
     else:

@@ -98,8 +98,16 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
  * 16-token tiles of all (sequence, KV head) pairs are shared out as equal runs
  * over `waves` waves, and a pair whose tiles span several runs is merged by
  * log-sum-exp (:191-204) in a second kernel on the same stream.  Wider query
- * blocks (up to 2^24 rows per KV head) run on an MFMA prefill kernel, 128
- * rows per workgroup, that needs no workspace and ignores `waves`.
+ * blocks (up to 2^24 rows per KV head) run on an MFMA prefill kernel, 256
+ * rows per workgroup (128 at head_dim > 128), that needs no workspace.
+ * Mixed batches (the reference pads decode and prefill rows into one call,
+ * engine/paged.py:345-346, :384-389): in a wide call with `widths`, the
+ * sequences whose width fits the decode kernel (at most 32 / (H/HK) queries,
+ * 16 / (H/HK) at head_dim > 128) are served by the split-K decode kernel and
+ * the others by the prefill kernel, in the same call; `waves` and the
+ * workspace then size that decode part (pkv_attention_workspace_bytes gives
+ * its size for the wide call's arguments).  Without room for its partials the
+ * prefill kernel serves every sequence.
  *
  *  queries      : [batch][num_heads][num_queries][head_dim], float_kind
  *  seq_lens     : [batch] tokens in each sequence's cache (after the append)
@@ -155,8 +163,9 @@ int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t
 int32_t pkv_attention_default_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries,
                                     int32_t batch);
 
-/* Workspace bytes pkv_paged_attention needs for `waves` work waves (0 for
- * query blocks served by the prefill kernel). */
+/* Workspace bytes pkv_paged_attention needs for `waves` work waves.  For
+ * query blocks served by the prefill kernel: the partials of a mixed batch's
+ * decode part (0 when the GQA ratio leaves the decode kernel no query). */
 int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_heads,
                                       int32_t num_queries, int32_t waves);
 

@@ -81,6 +81,15 @@ int cached_waves(const pkv_geometry &geo, int rows) {
   return w;
 }
 
+// Most queries per sequence the split-K decode kernel serves at this GQA
+// ratio (its row limit is 32 query rows per KV head, 16 at head_dim > 128);
+// 0 when not even one.
+int decode_queries(const pkv_geometry &geo, int gqa) {
+  int q = 32 / std::max(gqa, 1);
+  while (q > 0 && !pkv::decode_serves(pkv::to_geo(geo), q * gqa)) --q;
+  return q;
+}
+
 }  // namespace
 
 extern "C" {
@@ -168,7 +177,11 @@ int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_head
     return -1;
   const int64_t rows = (int64_t)num_queries * (num_heads / g.hk);
   if (rows > kMaxRows) return -1;
-  if (!pkv::decode_serves(pkv::to_geo(g), (int)rows)) return 0;  // prefill kernel: no partials
+  if (!pkv::decode_serves(pkv::to_geo(g), (int)rows)) {
+    // prefill kernel: no partials, except for the decode part of a mixed batch
+    const int gqa = num_heads / g.hk;
+    return workspace_parts(g, (int64_t)decode_queries(g, gqa) * gqa, waves).total;
+  }
   return workspace_parts(g, rows, waves).total;
 }
 
@@ -204,48 +217,53 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
   const int64_t tiles_per_seq = std::max<int64_t>(1, ((int64_t)max_pages * geo.page + 15) / 16) + 16;
   if ((int64_t)batch * tiles_per_seq * geo.hk > INT32_MAX / 2)
     return fail(PKV_UNSUPPORTED, "paged attention batch too large (more than 2^30 tiles)");
-  if (!pkv::decode_serves(pkv::to_geo(geo), rows)) {
-    // wide query blocks (chunked prefill): one pass per (sequence, KV head,
-    // 128-row block), no partials; waves and the workspace are not used
-    if ((int64_t)batch * geo.hk * ((rows + 127) / 128) > INT32_MAX)
-      return fail(PKV_UNSUPPORTED, "paged attention grid too large");
-    pkv::AttnArgs a;
-    a.g = pkv::to_geo(geo);
-    a.pool = (const uint8_t *)pool;
-    a.num_pages = num_pages;
-    a.q = (const uint16_t *)queries;
-    a.batch = batch;
-    a.heads = num_heads;
-    a.nq = num_queries;
-    a.gqa = gqa;
-    a.rows = rows;
-    a.table = block_table;
-    a.max_pages = max_pages;
-    a.seq_lens = seq_lens;
-    a.q_pos = q_pos;
-    a.widths = widths;
-    a.scale_log2 = scale * 1.4426950408889634f;
-    a.waves = 0;
-    a.lead = 0;
-    a.part_ml = nullptr;
-    a.part_acc = nullptr;
-    a.out = (uint16_t *)out;
-    return check_launch(pkv::launch_prefill((hipStream_t)stream, a), "prefill launch");
+  const bool wide = !pkv::decode_serves(pkv::to_geo(geo), rows);
+  if (wide && (int64_t)batch * geo.hk * ((rows + 127) / 128) > INT32_MAX)
+    return fail(PKV_UNSUPPORTED, "paged attention grid too large");
+  // The split-K decode parts: every sequence of a decode / verify call; in a
+  // wide call with per-sequence widths (a mixed batch), the sequences whose
+  // width fits the decode kernel -- in two tiers, those of at most 4 query
+  // rows per KV head (the 4-row column-slot kernel) and the wider ones up to
+  // the kernel's limit, so decode rows do not run at verify cost -- when the
+  // workspace holds each tier's partials (else the prefill kernel serves
+  // every sequence).  The tiers run one after the other on the stream and
+  // share the workspace.
+  struct Part {
+    int nq, lo, hi, waves;  // queries covered; serve widths in (lo, hi] (hi 0: all)
+    WorkspaceParts ws;
+  };
+  Part part[2];
+  int nparts = 0;
+  if (!wide) {
+    part[nparts++] = Part{num_queries, 0, 0, waves, {0, 0, 0}};
+  } else if (widths) {
+    const int hi = decode_queries(geo, gqa);
+    const int lo = std::min(hi, 4 / std::max(gqa, 1));
+    if (lo >= 1) part[nparts++] = Part{lo, 0, lo, waves, {0, 0, 0}};
+    if (hi > lo) part[nparts++] = Part{hi, lo, hi, waves, {0, 0, 0}};
   }
-  if (waves <= 0) {
-    waves = pkv_attention_default_waves(layout, num_heads, num_queries, batch);
-    if (waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
-    if (fit_waves) {
-      while (waves > 1 && workspace_parts(geo, rows, waves).total > workspace_bytes)
-        waves = std::max<int64_t>(1, std::min<int64_t>(waves - 1,
-            (int64_t)waves * workspace_bytes / workspace_parts(geo, rows, waves).total));
+  for (int i = 0; i < nparts; ++i) {
+    Part &t = part[i];
+    const int trows = t.nq * gqa;
+    if (t.waves <= 0) {
+      t.waves = pkv_attention_default_waves(layout, num_heads, t.nq, batch);
+      if (t.waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
+      if (fit_waves) {
+        while (t.waves > 1 && workspace_parts(geo, trows, t.waves).total > workspace_bytes)
+          t.waves = std::max<int64_t>(1, std::min<int64_t>(t.waves - 1,
+              (int64_t)t.waves * workspace_bytes / workspace_parts(geo, trows, t.waves).total));
+      }
+    }
+    if (t.waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
+    t.ws = workspace_parts(geo, trows, t.waves);
+    if (!workspace || workspace_bytes < t.ws.total) {
+      if (!wide)
+        return fail(PKV_OUT_OF_MEMORY,
+                    "attention workspace too small: need " + std::to_string(t.ws.total) + " bytes");
+      nparts = 0;  // no room: the prefill kernel serves every sequence
+      break;
     }
   }
-  if (waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
-  const WorkspaceParts parts = workspace_parts(geo, rows, waves);
-  if (!workspace || workspace_bytes < parts.total)
-    return fail(PKV_OUT_OF_MEMORY,
-                "attention workspace too small: need " + std::to_string(parts.total) + " bytes");
 
   pkv::AttnArgs a;
   a.g = pkv::to_geo(geo);
@@ -254,38 +272,63 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
   a.q = (const uint16_t *)queries;
   a.batch = batch;
   a.heads = num_heads;
-  a.nq = num_queries;
   a.gqa = gqa;
-  a.rows = rows;
   a.table = block_table;
   a.max_pages = max_pages;
   a.seq_lens = seq_lens;
   a.q_pos = q_pos;
   a.widths = widths;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.waves = waves;
-  a.lead = pkv::attention_lead(a.g, rows);
-  a.part_ml = (float *)((char *)workspace + parts.ml);
-  a.part_acc = (float *)((char *)workspace + parts.acc);
+  a.nq_stride = num_queries;
   a.out = (uint16_t *)out;
-  if (int rc = check_launch(pkv::launch_attention((hipStream_t)stream, a), "attention launch")) return rc;
-  pkv::MergeArgs m;
-  m.batch = batch;
-  m.hk = geo.hk;
-  m.heads = num_heads;
-  m.nq = num_queries;
-  m.gqa = gqa;
-  m.rows = rows;
-  m.dim = geo.dim;
-  m.dp = geo.dp;
-  m.float_kind = geo.float_kind;
-  m.waves = waves;
-  m.lead = a.lead;
-  m.seq_lens = seq_lens;
-  m.part_acc = a.part_acc;
-  m.part_ml = a.part_ml;
-  m.out = (uint16_t *)out;
-  return check_launch(pkv::launch_merge((hipStream_t)stream, m), "merge launch");
+  if (wide) {
+    // chunked prefill: one pass per (sequence, KV head, row block), no
+    // partials; sequences left to the decode parts get zeros, overwritten by them
+    a.nq = num_queries;
+    a.rows = rows;
+    a.narrow_lo = 0;
+    a.narrow_q = nparts ? part[nparts - 1].hi : 0;
+    a.waves = 0;
+    a.lead = 0;
+    a.part_ml = nullptr;
+    a.part_acc = nullptr;
+    if (int rc = check_launch(pkv::launch_prefill((hipStream_t)stream, a), "prefill launch")) return rc;
+  }
+  for (int i = 0; i < nparts; ++i) {
+    const Part &t = part[i];
+    a.nq = t.nq;
+    a.rows = t.nq * gqa;
+    a.narrow_lo = t.lo;
+    a.narrow_q = t.hi;
+    a.waves = t.waves;
+    a.lead = pkv::attention_lead(a.g, a.rows);
+    a.part_ml = (float *)((char *)workspace + t.ws.ml);
+    a.part_acc = (float *)((char *)workspace + t.ws.acc);
+    if (int rc = check_launch(pkv::launch_attention((hipStream_t)stream, a), "attention launch"))
+      return rc;
+    pkv::MergeArgs m;
+    m.batch = batch;
+    m.hk = geo.hk;
+    m.heads = num_heads;
+    m.nq = a.nq;
+    m.gqa = gqa;
+    m.rows = a.rows;
+    m.dim = geo.dim;
+    m.dp = geo.dp;
+    m.float_kind = geo.float_kind;
+    m.waves = t.waves;
+    m.lead = a.lead;
+    m.nq_stride = num_queries;
+    m.narrow_lo = t.lo;
+    m.narrow_q = t.hi;
+    m.seq_lens = seq_lens;
+    m.widths = widths;
+    m.part_acc = a.part_acc;
+    m.part_ml = a.part_ml;
+    m.out = (uint16_t *)out;
+    if (int rc = check_launch(pkv::launch_merge((hipStream_t)stream, m), "merge launch")) return rc;
+  }
+  return PKV_OK;
 }
 
 // ---- the allocation-free attention entry point ------------------------------------

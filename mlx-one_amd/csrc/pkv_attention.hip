@@ -127,14 +127,15 @@ __device__ __forceinline__ SegPieces seg_pieces(const Split &sp, int sv, int s0,
   return p;
 }
 
-// Total tiles of a launch (wave-uniform): hk * sum over sequences of seq_tiles.
-__device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int hk, int lane) {
-  int t = 0;
-  for (int c0 = 0; c0 < batch; c0 += 64) {
-    const int idx = c0 + lane;
-    t += wave_sum(idx < batch ? seq_tiles(lens[idx]) : 0);
-  }
-  return __builtin_amdgcn_readfirstlane(t) * hk;
+// Tiles the split gives sequence idx (< batch): seq_tiles, or none for a
+// sequence of a mixed batch that the prefill kernel serves (its width is past
+// narrow_q, the query rows this launch covers).  Served sequences have at
+// least one tile, so "served" is "tiles > 0", and only they are charged lead
+// tiles.
+__device__ __forceinline__ int split_tiles(const int32_t *lens, const int32_t *widths, int narrow_lo,
+                                           int narrow_q, int idx) {
+  if (narrow_q > 0 && (widths[idx] > narrow_q || widths[idx] <= narrow_lo)) return 0;
+  return seq_tiles(lens[idx]);
 }
 
 // The lead tiles a launch's split charges ahead of each segment: `lead`, or
@@ -142,16 +143,17 @@ __device__ __forceinline__ int total_tiles(const int32_t *lens, int batch, int h
 // boundaries (every sequence's tile count a multiple of the run length), so
 // that no run crosses one.  nt0: the lane's tile count in the first
 // 64-sequence chunk; t0: the lead-free tile total over all segments.
-__device__ __forceinline__ int charged_lead(const int32_t *lens, int batch, int waves, int lead,
-                                            int nt0, int t0, int lane) {
-  if (lead == 0) return 0;
+__device__ __forceinline__ int charged_lead(const int32_t *lens, const int32_t *widths, int narrow_lo,
+                                            int narrow_q, int batch, int waves, int lead, int nt0,
+                                            int t0, int lane) {
+  if (lead == 0 || t0 == 0) return 0;
   const int w0 = min(waves, t0);
   if (t0 % w0) return lead;
   const int q0 = t0 / w0;
   bool off = lane < batch && nt0 % q0 != 0;
   for (int c0 = 64; c0 < batch; c0 += 64) {
     const int idx = c0 + lane;
-    off |= idx < batch && seq_tiles(lens[idx]) % q0 != 0;
+    off |= idx < batch && split_tiles(lens, widths, narrow_lo, narrow_q, idx) % q0 != 0;
   }
   return __any(off) ? lead : 0;
 }
@@ -175,20 +177,26 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   const int unit = blockIdx.x;
   const int row = unit % a.rows, seg = unit / a.rows;
   const int b = seg / a.hk, kh = seg % a.hk;
-  // tiles before sequence b, and the launch's split (as the attention kernel made it)
-  int pre = 0, tiles = 0, nt0 = 0;
+  // tiles (and served sequences) before sequence b, and the launch's split
+  // (as the attention kernel made it)
+  int pre = 0, spre = 0, tiles = 0, served = 0, nt0 = 0;
   for (int c0 = 0; c0 < a.batch; c0 += 64) {
     const int idx = c0 + lane;
-    const int nt = idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0;
+    const int nt = idx < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, idx) : 0;
     if (c0 == 0) nt0 = nt;
     tiles += wave_sum(nt);
+    served += wave_sum(nt > 0 ? 1 : 0);
     pre += wave_sum(idx < b ? nt : 0);
+    spre += wave_sum(idx < b && nt > 0 ? 1 : 0);
   }
+  const int ntb = split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, b);
+  if (ntb == 0) return;  // served by the prefill kernel
   const int t0 = __builtin_amdgcn_readfirstlane(tiles) * a.hk;
-  const int lead = charged_lead(a.seq_lens, a.batch, a.waves, a.lead, nt0, t0, lane);
-  const int T = t0 + a.batch * a.hk * lead;
-  const int ntb = seq_tiles(a.seq_lens[b]);
-  const int sv = (__builtin_amdgcn_readfirstlane(pre) + b * lead) * a.hk + kh * (ntb + lead);
+  const int lead = charged_lead(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, a.batch, a.waves, a.lead, nt0,
+                                t0, lane);
+  const int T = t0 + __builtin_amdgcn_readfirstlane(served) * a.hk * lead;
+  const int sv = (__builtin_amdgcn_readfirstlane(pre) + __builtin_amdgcn_readfirstlane(spre) * lead) *
+                     a.hk + kh * (ntb + lead);
   Split sp;
   sp.init(T, min(a.waves, T));
   const SegPieces pc = seg_pieces(sp, sv, sv + lead, sv + lead + ntb);
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   __syncthreads();
   if (wv != 0) return;
   const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
-  uint16_t *o = a.out + (((int64_t)b * a.heads + h) * a.nq + qi) * a.dim;
+  uint16_t *o = a.out + (((int64_t)b * a.heads + h) * a.nq_stride + qi) * a.dim;
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
     const int d = lane * PER + e;
@@ -325,27 +333,30 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   auto scan_chunk = [&](int base, int pre) __attribute__((always_inline)) {
     cbase = base;
     chunk_pre = pre;
-    incl_l = wave_scan_incl(base + lane < a.batch ? nt_l + lead : 0, lane) + pre;
+    incl_l = wave_scan_incl(base + lane < a.batch && nt_l > 0 ? nt_l + lead : 0, lane) + pre;
     chunk_end = __builtin_amdgcn_readlane(incl_l, 63);
   };
   auto load_chunk = [&](int base, int pre) __attribute__((always_inline)) {
     const int idx = base + lane;
     len_l = idx < a.batch ? a.seq_lens[idx] : 0;
-    nt_l = idx < a.batch ? seq_tiles(len_l) : 0;
+    nt_l = idx < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, idx) : 0;
     scan_chunk(base, pre);
   };
   len_l = lane < a.batch ? a.seq_lens[lane] : 0;
-  nt_l = lane < a.batch ? seq_tiles(len_l) : 0;
-  int all_tiles = wave_sum(nt_l);
+  nt_l = lane < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, lane) : 0;
+  int all_tiles = wave_sum(nt_l), served = wave_sum(nt_l > 0 ? 1 : 0);
   for (int c0 = 64; c0 < a.batch; c0 += 64) {
     const int idx = c0 + lane;
-    all_tiles += wave_sum(idx < a.batch ? seq_tiles(a.seq_lens[idx]) : 0);
+    const int nt = idx < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, idx) : 0;
+    all_tiles += wave_sum(nt);
+    served += wave_sum(nt > 0 ? 1 : 0);
   }
   // tile counts fit in int32: the host bounds batch * (max_pages * pages' tiles + 16) * HK
   const int t0 = __builtin_amdgcn_readfirstlane(all_tiles) * hk;
-  lead = charged_lead(a.seq_lens, a.batch, a.waves, a.lead, nt_l, t0, lane);
+  if (t0 == 0) return;  // every sequence is served by the prefill kernel
+  lead = charged_lead(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, a.batch, a.waves, a.lead, nt_l, t0, lane);
   scan_chunk(0, 0);
-  const int T = t0 + a.batch * hk * lead;
+  const int T = t0 + __builtin_amdgcn_readfirstlane(served) * hk * lead;
   const int W = min(a.waves, T);
   if (w >= W) return;
   Split sp;
@@ -382,7 +393,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       const int row = SLOTS > 1 ? rowc : rb * 16 + col;
       const int rowv = row < a.rows ? row : 0;  // rows past the block load row 0, zeroed later
       const int qi = rowv / a.gqa, h = pkh * a.gqa + rowv % a.gqa;
-      const uint16_t *qrow = a.q + (((int64_t)pb * a.heads + h) * a.nq + qi) * g.dim;
+      const uint16_t *qrow = a.q + (((int64_t)pb * a.heads + h) * a.nq_stride + qi) * g.dim;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int d0 = 32 * kb + 8 * jj;
@@ -396,7 +407,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
                            (uint32_t)e8[4] | ((uint32_t)e8[5] << 16), (uint32_t)e8[6] | ((uint32_t)e8[7] << 16)};
         }
       }
-      qp[rb] = a.q_pos ? a.q_pos[(int64_t)pb * a.nq + qi] : 0;
+      qp[rb] = a.q_pos ? a.q_pos[(int64_t)pb * a.nq_stride + qi] : 0;
     }
   };
 
@@ -849,7 +860,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       const bool writer = slot_l == 0 && row < a.rows;
       const int qi = row / a.gqa, h = ckh * a.gqa + row % a.gqa;
       const float inv = 1.0f / fmaxf(lrow, 1e-20f);
-      uint16_t *o = a.out + (((int64_t)cb * a.heads + h) * a.nq + qi) * g.dim;
+      uint16_t *o = a.out + (((int64_t)cb * a.heads + h) * a.nq_stride + qi) * g.dim;
       float *pa = a.part_acc + ((int64_t)slot * a.rows + row) * DP;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {

@@ -34,8 +34,16 @@ struct AttnArgs {
   Geo g;
   const uint8_t *pool;
   int64_t num_pages;
-  const uint16_t *q;  // [B][H][Q][D]
+  const uint16_t *q;  // [B][H][nq_stride][D]
   int batch, heads, nq, gqa, rows;
+  // Q extent of queries, q_pos and out (= nq except for the decode part of a
+  // mixed batch, which covers the first nq of nq_stride query rows)
+  int nq_stride;
+  // Mixed batches (narrow_q 0: off).  Decode kernel: serve only sequences
+  // whose width w has narrow_lo < w <= narrow_q.  Prefill kernel: leave
+  // sequences of width at most narrow_q to the decode kernel (their rows are
+  // written as zeros first).
+  int narrow_lo, narrow_q;
   const int32_t *table;
   int max_pages;
   const int32_t *seq_lens, *q_pos, *widths;
@@ -50,7 +58,8 @@ struct AttnArgs {
 struct MergeArgs {
   int batch, hk, heads, nq, gqa, rows, dim, dp, float_kind;
   int waves, lead;  // as launched for the attention kernel
-  const int32_t *seq_lens;
+  int nq_stride, narrow_lo, narrow_q;
+  const int32_t *seq_lens, *widths;
   const float *part_acc, *part_ml;
   uint16_t *out;
 };

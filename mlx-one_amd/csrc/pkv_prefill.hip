@@ -90,15 +90,22 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   const Geo &g = a.g;
   // Blocks of one (sequence, KV head) read the same pages: give them
   // consecutive slots of one XCD (workgroups are dealt to the 8 XCDs
-  // round-robin) so the span is fetched into one L2.
-  int bid = blockIdx.x;
-  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  // round-robin) so the span is fetched into one L2.  XCD x runs segments
+  // x, x + 8, x + 16, ...: heavy segments that sit together in the batch (the
+  // prefill rows of a mixed batch) still spread over every XCD.
   const int nblk = (a.rows + ROWS - 1) / ROWS;
+  int bid = blockIdx.x;
+  if (((gridDim.x / nblk) & 7) == 0) {
+    const int x = bid & 7, k = bid >> 3;
+    bid = (x + 8 * (k / nblk)) * nblk + k % nblk;
+  }
   const int seg = bid / nblk, rblk = bid % nblk;
   const int b = seg / g.hk, kh = seg % g.hk;
   if (b >= a.batch) return;
   const int L = a.seq_lens[b];
-  const int width = a.widths ? a.widths[b] : a.nq;
+  // a sequence of a mixed batch that the decode kernel serves: zeros here,
+  // its rows are written by the decode kernel launched next on the stream
+  const int width = a.widths ? (a.narrow_q > 0 && a.widths[b] <= a.narrow_q ? 0 : a.widths[b]) : a.nq;
 
   // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];

@@ -130,6 +130,16 @@ def default_waves(fmt: PageFormat, num_heads, num_queries, batch):
     return waves
 
 
+def decode_queries(fmt: PageFormat, num_heads, num_queries):
+    """Queries per sequence of the split-K decode part of a call: all of them
+    when the decode kernel serves the call (at most 32 query rows per KV head,
+    16 at head_dim > 128), else the most a mixed batch's narrow sequences may
+    have there (0 when the GQA ratio leaves none)."""
+    gqa = num_heads // fmt.num_kv_heads
+    limit = 16 if fmt.stored_dim > 128 else 32
+    return num_queries if num_queries * gqa <= limit else limit // max(gqa, 1)
+
+
 def workspace_bytes(fmt: PageFormat, num_heads, num_queries, waves):
     return int(nat.load().pkv_attention_workspace_bytes(fmt.c_layout, num_heads, num_queries,
                                                           waves))
@@ -157,8 +167,11 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     ``seq_lens`` counts the tokens in each sequence's cache (after the
     append) and stays on the device: the decode kernel shares the tiles of
     all sequences out over ``waves`` waves (default: ``default_waves``);
-    query blocks past 32 rows per KV head run on the prefill kernel.
-    ``workspace`` (bytes from ``workspace_bytes``) may be given by the caller.
+    query blocks past 32 rows per KV head run on the prefill kernel -- and
+    in a mixed batch (``widths`` given), the sequences narrow enough for the
+    decode kernel still go to it, in the same call (``waves`` then sizes that
+    part).  ``workspace`` (bytes from ``workspace_bytes``) may be given by the
+    caller.
     """
     if queries.dim() != 4:
         raise ValueError("queries must be [B, H, Q, D]")
@@ -170,7 +183,7 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     table = _i32(block_table, device)
     lens = _i32(seq_lens, device)
     if waves <= 0:
-        waves = default_waves(fmt, heads, nq, batch)
+        waves = default_waves(fmt, heads, decode_queries(fmt, heads, nq) or nq, batch)
     need = workspace_bytes(fmt, heads, nq, waves)
     if need < 0:
         nat.check(nat.PKV_INVALID_ARGUMENT, "paged attention workspace")

@@ -36,6 +36,21 @@ class Workload:
     fixed_chunk: bool = False      # every step re-appends the same chunk (fixed shape)
     seed: int = 0
     description: str = ""
+    widths: tuple = ()             # per-sequence query rows (mixed batches); () = num_queries
+    tail_lengths: tuple = ()       # fixed lengths of the last sequences after the drawn ones
+
+    def step_widths(self):
+        """Query rows of each sequence in one step (its last tokens)."""
+        if self.widths:
+            return np.asarray(self.widths, np.int64)
+        return np.full(self.batch, self.num_queries, np.int64)
+
+    def step_appends(self):
+        """Tokens each sequence appends in one step (a mixed batch appends its
+        query rows)."""
+        if self.widths:
+            return np.asarray(self.widths, np.int64)
+        return np.full(self.batch, self.append_tokens, np.int64)
 
 
 CONFIGS = {
@@ -62,6 +77,15 @@ CONFIGS = {
                    description="int8 G64 chunked prefill: 512-token causal query chunk per "
                                "sequence over a 4096-token paged prefix plus the chunk, B4 "
                                "H32/HK8 D128 P16"),
+    # C2's decode rows and C5's prefill chunks in one padded batch (the
+    # reference pads mixed widths into one forward, engine/paged.py:345-346)
+    "mixed": Workload("mixed", batch=36, heads=32, kv_heads=8, head_dim=128, page_tokens=16,
+                      bits=8, group_size=64, num_queries=512, append_tokens=512,
+                      length_range=(1024, 8192), tail_lengths=(4096,) * 4,
+                      widths=(1,) * 32 + (512,) * 4, outlier_fraction=0.01, fixed_chunk=True,
+                      seed=5,
+                      description="mixed batch, int8 G64: 32 decode rows (L~U[1024,8192]) and "
+                                  "4 prefill chunks of 512 over 4096 cached tokens, one call"),
 }
 
 
@@ -99,15 +123,20 @@ class Instance:
     num_pages: int = 0
 
     @property
+    def widths(self):
+        return self.workload.step_widths().astype(np.int32)
+
+    @property
     def total_lengths(self):
-        return self.context + self.workload.append_tokens
+        return self.context + self.workload.step_appends()
 
     @property
     def positions(self):
-        """Logical positions of the query rows: the last Q tokens of each sequence."""
+        """Logical positions of the query rows: a sequence's ``width`` rows are
+        its last tokens, padding rows continue after them."""
         w = self.workload
-        return np.stack([np.arange(n - w.num_queries, n) for n in self.total_lengths]).astype(
-            np.int32)
+        return np.stack([np.arange(n - q, n - q + w.num_queries)
+                         for n, q in zip(self.total_lengths, w.step_widths())]).astype(np.int32)
 
 
 def generate(w: Workload, *, extra_tokens=0, layer=0, kv=True):
@@ -121,8 +150,9 @@ def generate(w: Workload, *, extra_tokens=0, layer=0, kv=True):
         context = np.asarray(w.lengths, np.int64)
     else:
         lo, hi = w.length_range
-        context = rng.integers(lo, hi, size=w.batch, endpoint=True).astype(np.int64)
-    total = context + w.append_tokens
+        drawn = rng.integers(lo, hi, size=w.batch - len(w.tail_lengths), endpoint=True)
+        context = np.concatenate([drawn, np.asarray(w.tail_lengths, np.int64)]).astype(np.int64)
+    total = context + w.step_appends()
     capacity = total + extra_tokens
     pages_per = (capacity + w.page_tokens - 1) // w.page_tokens
     # a shared prefix cannot be longer than the shortest sequence's full pages

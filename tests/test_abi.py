@@ -76,8 +76,17 @@ def test_workspace_size():
     assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 0) < 0     # no waves
     assert lib.pkv_attention_workspace_bytes(_layout(), 30, 1, 10) < 0    # not GQA groups
     # query blocks past the decode kernel's 32 rows per KV head run on the
-    # prefill kernel: no split, no partials
-    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 9, 10) == 0
+    # prefill kernel, except a mixed batch's sequences of at most 8 queries
+    # (32 rows at GQA 4): partials for those only
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 9, 10) == \
+        lib.pkv_attention_workspace_bytes(_layout(), 32, 8, 10)
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 512, 10) == \
+        lib.pkv_attention_workspace_bytes(_layout(), 32, 8, 10)
+    # head_dim 256: 16 rows, 4 queries at GQA 4; none at GQA 32
+    assert lib.pkv_attention_workspace_bytes(_layout(head_dim=256, group_size=128), 32, 64, 10) \
+        == lib.pkv_attention_workspace_bytes(_layout(head_dim=256, group_size=128), 32, 4, 10)
+    assert lib.pkv_attention_workspace_bytes(_layout(head_dim=256, group_size=128), 256, 1,
+                                             10) == 0
     assert lib.pkv_attention_waves(_layout(), 32, 512) == 1
     assert lib.pkv_attention_waves(_layout(head_dim=256), 32, 5) == 1     # 20 rows at D=256
     assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1 << 23, 10) < 0

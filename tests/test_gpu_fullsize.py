@@ -127,7 +127,7 @@ def run_config(name, *, waves_of=None):
     inst = workloads.generate(w)
     fmt = _fmt(w)
     context = inst.context.astype(np.int64)
-    total = context + w.append_tokens
+    total = inst.total_lengths.astype(np.int64)
     pool = ops.allocate_pool(fmt, inst.num_pages)
     append(fmt, pool, w, inst.keys, inst.values, inst.table, np.zeros_like(context), context)
     if w.append_tokens:                       # the step's own append of its new tokens
@@ -136,16 +136,17 @@ def run_config(name, *, waves_of=None):
     positions = inst.positions
     scale = 1.0 / math.sqrt(w.head_dim)
     waves = waves_of(w, total) if waves_of else 0
+    widths = torch.from_numpy(inst.widths).cuda() if w.widths else None
     out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype),
                               torch.from_numpy(inst.table).cuda(), lengths, scale=scale,
-                              q_pos=torch.from_numpy(positions).cuda(), waves=waves)
+                              q_pos=torch.from_numpy(positions).cuda(), widths=widths,
+                              waves=waves)
     torch.cuda.synchronize()
     arrays, counts = oracle_arrays(w, inst.keys, inst.values, inst.table, inst.num_pages)
     pages = check_pages_bit_exact(fmt, pool, arrays, counts)
-    want = cport.paged_attention(inst.queries, inst.table, total, positions,
-                                 np.full(w.batch, w.num_queries, np.int32), heads_kv=w.kv_heads,
-                                 page_tokens=w.page_tokens, bits=w.bits, group_size=w.group_size,
-                                 pages=arrays, scale=scale)
+    want = cport.paged_attention(inst.queries, inst.table, total, positions, inst.widths,
+                                 heads_kv=w.kv_heads, page_tokens=w.page_tokens, bits=w.bits,
+                                 group_size=w.group_size, pages=arrays, scale=scale)
     worst, mean, over = assert_attention_close_f32(out.float().cpu().numpy(), want)
     print(f"{name}: {pages} pages bit-exact, {int(total.sum())} tokens; attention max abs "
           f"{worst:.2e}, mean abs {mean:.2e}, {over} elements over 2e-2")
@@ -174,6 +175,14 @@ def test_c5_full_size_chunked_prefill():
     run_config("c5")
 
 
+def test_mixed_full_size_decode_and_prefill_rows_in_one_call():
+    """C2's 32 decode rows and C5's 4 prefill chunks padded into one batch of
+    512 query rows: one call serves the decode rows on the split-K kernel and
+    the chunks on the prefill kernel; padded rows are zero."""
+    out = run_config("mixed")
+    assert not out[:32, :, 1:].any()
+
+
 def test_c4_full_size_verify_over_a_refcounted_shared_prefix():
     """B16 verify, 5 causal drafts, L ~ U[512, 4096]: sequence 0 writes the
     256-token prefix into the device arena, the fifteen others fork it (each
@@ -186,7 +195,7 @@ def test_c4_full_size_verify_over_a_refcounted_shared_prefix():
     inst = workloads.generate(w)
     fmt = _fmt(w)
     context = inst.context.astype(np.int64)
-    total = context + w.append_tokens
+    total = inst.total_lengths.astype(np.int64)
     prefix = w.shared_prefix_pages * w.page_tokens
     distinct = int(sum(-(-int(n) // w.page_tokens) for n in total)) - \
         (w.batch - 1) * w.shared_prefix_pages

@@ -346,6 +346,60 @@ def test_attention_ignores_stale_bytes_of_reused_pages(bits, nq, dtype):
         assert_attention_close(out.float().cpu().numpy(), want)
 
 
+MIXED_CASES = {
+    # name: (workload overrides); widths per sequence, Q = their maximum
+    "c2_c5_int8": dict(name="c5", batch=6, lengths=(300, 40, 1000, 90, 2, 700), num_queries=64,
+                       append_tokens=64, widths=(1, 64, 1, 3, 1, 17)),
+    "verify_rows_gqa4": dict(name="c5", batch=5, lengths=(130, 500, 64, 9, 333), num_queries=40,
+                             append_tokens=40, widths=(5, 40, 8, 1, 9)),
+    "gqa8_4bit_p32": dict(name="c5", batch=4, heads=64, lengths=(200, 1000, 50, 77),
+                          num_queries=36, append_tokens=36, bits=4, page_tokens=32,
+                          widths=(4, 36, 1, 2)),
+    "d256_four_queries": dict(name="c5", batch=4, lengths=(90, 300, 17, 128), head_dim=256,
+                              group_size=128, num_queries=20, append_tokens=20,
+                              widths=(4, 20, 1, 5)),
+    "bf16_pages_many_decode": dict(name="c5", batch=70, lengths=(), length_range=(1, 600),
+                                   num_queries=48, append_tokens=48, bits=16,
+                                   widths=(48, 1, 2, 3, 7) * 14),
+}
+
+
+@pytest.mark.parametrize("case", sorted(MIXED_CASES))
+def test_mixed_batch_routes_rows_per_sequence(case):
+    """One call over sequences of different widths: the ones the decode kernel
+    serves (at most 32 query rows per KV head) go to it, the others to the
+    prefill kernel; both against the oracle, padded rows zero.  With no room
+    for the decode part's partials, the prefill kernel serves every sequence
+    (same result within the bar)."""
+    from pkv import ops, workloads
+
+    overrides = dict(MIXED_CASES[case])
+    w = workloads.get(overrides.pop("name"), **overrides)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    scale = scale_of(w.head_dim)
+    q = to_torch(inst.queries, fmt.dtype)
+    widths = torch.from_numpy(inst.widths).cuda()
+    want = oracle_attention(fmt, inst, inst.positions, inst.widths, scale)
+    outs = []
+    for q_pos in (torch.from_numpy(inst.positions).cuda(), None):
+        for waves in (0, 5):
+            out = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
+                                      widths=widths, waves=waves)
+            torch.cuda.synchronize()
+            assert_attention_close(out.float().cpu().numpy(), want)
+            outs.append(out)
+    tiny = torch.empty(256, dtype=torch.uint8, device="cuda")    # no decode part
+    alone = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, widths=widths,
+                                workspace=tiny, waves=5)
+    torch.cuda.synchronize()
+    assert_attention_close(alone.float().cpu().numpy(), want)
+    got = outs[0].float().cpu().numpy()
+    for b, n in enumerate(inst.widths):
+        assert not got[b, :, n:].any(), b
+
+
 def test_attention_padded_query_rows_are_zero():
     from pkv import ops, workloads
 
