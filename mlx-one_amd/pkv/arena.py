@@ -12,6 +12,7 @@ buffers alive for a dispatch, ``stats`` reports the same keys.
 
 from __future__ import annotations
 
+import heapq
 import weakref
 from contextlib import contextmanager
 
@@ -39,12 +40,13 @@ def page_format(layout):
 class DevicePagePool:
     """Pages of one layout in one device buffer ``[capacity, page_bytes]`` (uint8).
 
-    Grows by doubling (copying the live pages, zero-filling the rest, so that
-    unwritten token slots of a page are finite); freed pages are reused
-    lowest-id first.
+    Grows by doubling (copying the live pages, zero-filling the rest), never
+    past ``max_pages`` -- the arena's byte budget in pages of this layout -- so
+    the buffer stays within the configured bytes; freed pages are reused
+    lowest-id first (a heap).
     """
 
-    def __init__(self, fmt, device, ordinal, initial_pages=64):
+    def __init__(self, fmt, device, ordinal, initial_pages=64, max_pages=None):
         self.fmt, self.device, self.ordinal = fmt, device, ordinal
         self.page_bytes = fmt.page_bytes
         self.buffer = None
@@ -52,11 +54,14 @@ class DevicePagePool:
         self.next_page = 0
         self.free = []
         self.initial_pages = initial_pages
+        self.max_pages = max_pages
 
     def _grow(self, need):
         import torch
 
         capacity = max(self.initial_pages, self.capacity * 2, need)
+        if self.max_pages is not None:
+            capacity = max(min(capacity, self.max_pages), need)
         buffer = torch.zeros((capacity, self.page_bytes), dtype=torch.uint8, device=self.device)
         if self.buffer is not None:
             buffer[:self.capacity].copy_(self.buffer)
@@ -64,15 +69,14 @@ class DevicePagePool:
 
     def take(self):
         if self.free:
-            self.free.sort(reverse=True)
-            return self.free.pop()
+            return heapq.heappop(self.free)
         if self.next_page >= self.capacity:
             self._grow(self.next_page + 1)
         self.next_page += 1
         return self.next_page - 1
 
     def give(self, page):
-        self.free.append(page)
+        heapq.heappush(self.free, page)
 
     @property
     def live_pages(self):
@@ -96,7 +100,9 @@ class SegmentedPageArena(BlockPool):
     def pool_for(self, layout) -> DevicePagePool:
         pool = self.pools.get(layout)
         if pool is None:
-            pool = DevicePagePool(page_format(layout), self.device, len(self.pools))
+            fmt = page_format(layout)
+            pool = DevicePagePool(fmt, self.device, len(self.pools),
+                                  max_pages=max(1, self.capacity_bytes // fmt.page_bytes))
             self.pools[layout] = pool
         return pool
 

@@ -199,3 +199,21 @@ def test_profiled_traffic_matches_algorithmic_bytes():
     inst = workloads.generate(w, kv=False)
     attn, _ = bench.algorithmic_bytes(w, inst.context + w.append_tokens)
     assert 1.0 <= traffic / attn < 1.05
+
+
+def test_page_pool_stays_within_the_byte_budget_and_reuses_lowest_ids():
+    """A pool grows by doubling but never past the arena's budget in pages;
+    freed pages come back lowest id first."""
+    arena = SegmentedPageArena(10 * 34816, block_tokens=16, device="cpu")   # 10 C2 pages
+    cache = _cache(arena, bits=8, group=64)
+    layout = cache.layout_for(8, 128)
+    pool = arena.pool_for(layout)
+    assert pool.page_bytes == 34816 and pool.max_pages == 10
+    _plan(cache, 160, heads=8, dim=128)                  # 10 pages: the whole budget
+    assert pool.capacity == 10 and pool.buffer.shape[0] == 10
+    with pytest.raises(CacheCapacityError):
+        _plan(cache, 1, heads=8, dim=128)
+    freed = [cache._blocks[i].block.page for i in (7, 3, 5)]
+    for i in sorted((7, 3, 5), reverse=True):
+        cache._blocks.pop(i).close()
+    assert [pool.take() for _ in range(3)] == sorted(freed)
