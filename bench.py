@@ -359,18 +359,22 @@ def layer_bench(args):
 
 
 def layer_device_bench(args):
-    """The same layer decode steps with the page bookkeeping on the device
-    (``DevicePageArena`` + ``DeviceRunner``): one reservation kernel per step
-    instead of per-sequence host page tables.  With ``--graph`` each timed step
-    is one replay of a captured decode step (reserve, QKV GEMM, RoPE, append,
-    attention, merge, output GEMM); otherwise an eager ``DeviceRunner.execute``."""
+    """The same layer decode steps through the same reference-named calls
+    (``CacheManager.create_handle`` + ``PagedRunner.execute``) with the page
+    bookkeeping on the device: ``CacheConfig(page_arena="device")`` gives each
+    handle a ``DevicePageArena`` slot, so a step is one reservation kernel
+    instead of per-sequence host page tables.  With ``--graph`` the runner
+    replays repeated decode steps of the same sequences as captured HIP graphs
+    (reservation, then QKV GEMM, RoPE, append, attention, merge, output GEMM),
+    reading the reservation's error bits between the two."""
     import numpy as np
     import torch
 
     from pkv import _native, workloads
-    from pkv.device_arena import DevicePageArena, DeviceRunner
+    from pkv.cache_manager import CacheConfig, CacheManager
     from pkv.layer import AttentionStack, ModelSpec
     from pkv.ops import PageFormat
+    from pkv.runner import ForwardRequest, PagedRunner
 
     _native.load()
     device = torch.device("cuda:0")
@@ -382,50 +386,52 @@ def layer_device_bench(args):
     fmt = PageFormat(w.kv_heads, w.head_dim, w.page_tokens, 8, w.group_size, torch.float16)
     context = [int(x) for x in inst.context]
     extra = args.warmup + args.steps + 2
-    longest = max(context) + extra
     pages = sum(-(-(c + extra) // w.page_tokens) for c in context) + w.batch
-    arena = DevicePageArena(fmt, pages, num_layers=1, max_slots=w.batch, max_tokens=longest,
-                            device=device)
-    runner = DeviceRunner(model, arena)
-    slots = [arena.open_slot() for _ in range(w.batch)]
+    cm = CacheManager(model, CacheConfig(block_size_tokens=w.page_tokens, key_type="q8_0",
+                                         value_type="q8_0", group_size=w.group_size,
+                                         memory_budget_bytes=64 << 30, device_pages=pages,
+                                         page_arena="device", max_sequences=w.batch,
+                                         max_sequence_tokens=max(context) + extra),
+                      device=device)
+    handles = [cm.create_handle(f"seq{b}", key_type="q8_0", value_type="q8_0")
+               for b in range(w.batch)]
+    runner = PagedRunner(model, graphs=bool(args.graph))
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
+
+    def requests(rows, hidden, phase):
+        return [ForwardRequest(handles[b].request_id, x, handles[b].bundle.entries, phase=phase,
+                               runtime=cm, handle=handles[b]) for b, x in zip(rows, hidden)]
+
     chunk = 1024
     while True:
-        left = [c - arena.lengths[s] for c, s in zip(context, slots)]
+        left = [c - h.token_count for c, h in zip(context, handles)]
         rows = [b for b in range(w.batch) if left[b] > 0]
         if not rows:
             break
-        widths = [min(chunk, left[b]) for b in rows]
-        hidden = torch.randn((len(rows), max(widths), spec.hidden), generator=gen, device=device,
-                             dtype=torch.float16)
-        runner.execute([slots[b] for b in rows], hidden, widths)
-    arena.check()
+        hidden = [torch.randn((min(chunk, left[b]), spec.hidden), generator=gen, device=device,
+                              dtype=torch.float16) for b in rows]
+        runner.execute(requests(rows, hidden, "prefill"))
     decode_in = torch.randn((args.warmup + args.steps, w.batch, 1, spec.hidden), generator=gen,
                             device=device, dtype=torch.float16)
-    if args.graph:
-        x = decode_in[0].clone()
-        captured = runner.capture_decode(slots, x)      # runs one step eagerly
-        replay = captured.replay
-
-        def step(i):
-            x.copy_(decode_in[i])
-            replay()
-    else:
-        def step(i):
-            runner.execute(slots, decode_in[i])
-    for i in range(1, args.warmup):
-        step(i)
+    decode_in = [x.unbind(0) for x in decode_in.unbind(0)]
+    every = list(range(w.batch))
+    for i in range(args.warmup):
+        runner.execute(requests(every, decode_in[i], "decode"))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(args.warmup + i)
+        runner.execute(requests(every, decode_in[args.warmup + i], "decode"))
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / args.steps * 1e3
+    arena = handles[0].bundle.entries[0].arena
+    mirror = list(arena.lengths)
     arena.sync_lengths()
+    assert arena.lengths == mirror, "host length mirror differs from the device"
     arena.check()
     result = {
-        "metric": "e2e attention-layer decode tok/s (device page arena, Llama-3-8B layer, q8_0 KV)",
+        "metric": "e2e attention-layer decode tok/s (CacheManager + PagedRunner on the device "
+                  "page arena, Llama-3-8B layer, q8_0 KV)",
         "value": round(w.batch / (ms / 1e3), 1), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
@@ -434,7 +440,9 @@ def layer_device_bench(args):
                    "batch": w.batch, "hidden": spec.hidden, "heads": spec.query_heads,
                    "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "kv": "q8_0",
                    "group_size": w.group_size, "page_tokens": w.page_tokens,
-                   "mean_context": float(np.mean([arena.lengths[s] for s in slots]))},
+                   "mean_context": float(np.mean([h.token_count for h in handles]))},
+        "trace": {k: runner.last_trace.get(k) for k in ("page_arena", "graph_replay",
+                                                        "batch_size")},
     }
     print(json.dumps(result))
     return 0

@@ -46,6 +46,14 @@ class CacheConfig:
     ssd_cache_budget_bytes: int = 1 << 30
     ssd_staging_budget_bytes: int = 256 << 20
     ssd_max_entries: int = 128
+    # "host": pages owned by host bookkeeping (SegmentedPageArena + PagedKVCache,
+    # the reference's structure); "device": a DevicePageArena per precision,
+    # one sequence slot per handle (no host page bookkeeping per step)
+    page_arena: str = "host"
+    max_sequences: int = 256          # device arena: sequence slots
+    max_sequence_tokens: int = 32768  # device arena: tokens per slot
+    prefix_max_entries: int = 64      # device arena: published prefixes kept
+    device_pages: int = 0             # device arena: pages per layer (0: from the budget)
 
 
 @dataclass
@@ -100,7 +108,11 @@ class CacheManager:
     def __init__(self, bundle, config: CacheConfig = CacheConfig(), *, device="cuda"):
         if config.backend != "paged":
             raise ValueError("this build serves the paged backend only")
+        if config.page_arena not in ("host", "device"):
+            raise ValueError("page_arena must be 'host' or 'device'")
         self.bundle, self.config = bundle, config
+        self.device = device
+        self.device_arenas = {}    # (dtype, bits) -> (DevicePageArena, DevicePrefixIndex)
         self.block_pool = SegmentedPageArena(config.memory_budget_bytes,
                                              block_tokens=config.block_size_tokens, device=device)
         self.block_prefix = BlockPrefixIndex(config.prefix_cache_budget_bytes,
@@ -135,14 +147,68 @@ class CacheManager:
                 raise KVQuantizationUnsupported("paged KV requires matched precision")
             bits = _BITS[key_type]
             dtype = "bfloat16" if key_type == "bf16" else "float16"
-            entries = tuple(PagedKVCache(self.block_pool, layer_id=s.layer_id, dtype=dtype,
-                                         bits=bits, group_size=self.config.group_size)
-                            for s in self.layer_specs)
+            if self.config.page_arena == "device":
+                entries = self._slot_entries(dtype, bits)
+            else:
+                entries = tuple(PagedKVCache(self.block_pool, layer_id=s.layer_id, dtype=dtype,
+                                             bits=bits, group_size=self.config.group_size)
+                                for s in self.layer_specs)
             handle = CacheHandle(f"cache-{uuid.uuid4().hex}", request_id,
                                  sequence_id or request_id, CacheBundle(entries), "paged",
                                  key_type)
             self._handles[handle.handle_id] = handle
             return handle
+
+    # -- device arena ------------------------------------------------------------------
+    def _device_arena(self, dtype, bits):
+        """The DevicePageArena (and its prefix index) of one precision: every
+        layer's pool sized from the byte budget."""
+        key = (dtype, bits)
+        if key not in self.device_arenas:
+            import torch
+
+            from pkv.device_arena import DevicePageArena
+            from pkv.device_cache import DevicePrefixIndex
+            from pkv.ops import PageFormat
+
+            specs = self.layer_specs
+            if len({(s.num_kv_heads, s.key_head_dim, s.value_head_dim) for s in specs}) != 1:
+                raise CacheTopologyUnsupported("a device arena holds layers of one shape")
+            s0 = specs[0]
+            fmt = PageFormat(s0.num_kv_heads, s0.key_head_dim, self.config.block_size_tokens,
+                             bits or 16, self.config.group_size if bits else 32,
+                             getattr(torch, dtype))
+            per_page = fmt.page_bytes * len(specs)
+            capacity = self.config.device_pages or self.config.memory_budget_bytes // per_page
+            if capacity < 1:
+                raise CacheCapacityError("cache budget below one page per layer", retryable=False)
+            arena = DevicePageArena(fmt, capacity, num_layers=len(specs),
+                                    max_slots=self.config.max_sequences +
+                                    self.config.prefix_max_entries,
+                                    max_tokens=self.config.max_sequence_tokens,
+                                    device=self.device)
+            prefix = DevicePrefixIndex(arena, capacity_pages=max(
+                self.config.prefix_cache_budget_bytes // per_page, 0),
+                max_entries=self.config.prefix_max_entries)
+            self.device_arenas[key] = (arena, prefix)
+        return self.device_arenas[key]
+
+    def _slot_entries(self, dtype, bits):
+        from pkv.device_cache import SlotLayerCache
+        from pkv.paged import _layout
+
+        arena, _ = self._device_arena(dtype, bits)
+        slot = arena.open_slot()
+        return tuple(SlotLayerCache(arena, slot, s.layer_id, dtype, bits, self.config.group_size,
+                                    _layout(s.layer_id, self.config.block_size_tokens,
+                                            s.num_kv_heads, s.key_head_dim, dtype, bits,
+                                            self.config.group_size))
+                     for s in self.layer_specs)
+
+    @staticmethod
+    def _device_slot(handle):
+        first = handle.bundle.entries[0] if handle.bundle.entries else None
+        return first if first is not None and hasattr(first, "slot") else None
 
     def _validate_handle(self, handle):
         if handle.closed or self._handles.get(handle.handle_id) is not handle:
@@ -201,6 +267,17 @@ class CacheManager:
                 raise PrefixReuseUnsupported("multimodal prefix restoration is unavailable")
             if not self.config.prefix_cache_enabled:
                 return 0
+            view = self._device_slot(handle)
+            if view is not None:
+                _, prefix = self._device_arena(view.dtype, view.bits)
+                entry, pages = prefix.longest(fingerprint, tokens, minimum_tokens)
+                if entry is None:
+                    return 0
+                count = prefix.adopt(view.slot, entry, pages)
+                handle.token_count = count
+                handle.metadata["shared_blocks"] = pages
+                handle.metadata["prefix_tokens_reused"] = count
+                return count
             match = self.block_prefix.lookup(fingerprint, tuple(tokens),
                                              minimum_tokens=minimum_tokens)
             if match is None:
@@ -243,6 +320,13 @@ class CacheManager:
             if (handle.metadata.get("cancelled") or fingerprint.multimodal_identity is not None
                     or any(int(c.offset) != len(tokens) for c in handle.bundle.entries)):
                 return False
+            view = self._device_slot(handle)
+            if view is not None:
+                _, prefix = self._device_arena(view.dtype, view.bits)
+                stored = prefix.publish(view.slot, fingerprint, tokens)
+                handle.metadata["prefix_publications"] = (
+                    handle.metadata.get("prefix_publications", 0) + int(stored))
+                return stored
             layers = tuple(cache.full_block_refs for cache in handle.bundle.entries)
             stored = self.block_prefix.publish(fingerprint, tuple(tokens), layers) > 0
             handle.metadata["prefix_publications"] = (
@@ -339,6 +423,9 @@ class CacheManager:
             if handle.closed:
                 raise CacheCorruptionError("cache handle released twice")
             self._validate_handle(handle)
+            view = self._device_slot(handle)
+            if view is not None:
+                view.arena.release([view.slot])
             for entry in handle.bundle.entries:
                 entry.reset()
             if handle.reservation is not None:
@@ -348,14 +435,23 @@ class CacheManager:
 
     def stats(self):
         with self._lock:
+            arena = self.block_pool.stats()
+            allocated = self.block_pool.allocated_nbytes
+            for (dtype, bits), (dev, prefix) in self.device_arenas.items():
+                pages = dev.capacity * len(dev.pools)
+                allocated += pages * dev.fmt.page_bytes
+                arena[f"device_{dtype}_{bits or 16}"] = {
+                    "capacity_pages": dev.capacity, "layers": len(dev.pools),
+                    "page_bytes": dev.fmt.page_bytes, "prefix_entries": prefix.entries}
             return CacheMemoryStats(self.config.memory_budget_bytes, self._reserved,
-                                    self._transient, self.block_pool.allocated_nbytes,
-                                    len(self._handles), self.block_pool.stats())
+                                    self._transient, allocated, len(self._handles), arena)
 
     def close(self):
         with self._lock:
             for handle in list(self._handles.values()):
                 self.release(handle)
+            for _, prefix in self.device_arenas.values():
+                prefix.clear()
             self.block_prefix.clear()
             self.block_pool.clear()
             self._closed = True

@@ -210,10 +210,13 @@ class DevicePageArena:
     def error_probe(self):
         """Enqueue a copy of the error bits (as the stream stands now) into pinned
         host memory; ``probe_failed(probe)`` reads it once that point of the
-        stream has run -- usually long before the caller asks."""
-        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        stream has run -- usually long before the caller asks.  One probe at a
+        time per arena (its calls are ordered on one stream anyway): the pinned
+        word and the event are reused."""
+        if getattr(self, "_probe", None) is None:
+            self._probe = (torch.empty(1, dtype=torch.int32, pin_memory=True), torch.cuda.Event())
+        host, event = self._probe
         host.copy_(self.state[1:2], non_blocking=True)
-        event = torch.cuda.Event()
         event.record(torch.cuda.current_stream(self.device))
         return host, event
 
@@ -310,35 +313,51 @@ class DeviceRunner:
             self.arena._raise(err)
         return out
 
-    def capture_decode(self, slots, hidden):
-        """A graph of one decode step (one token per slot) reading the static
+    def capture_decode(self, slots, hidden, *, warm=True):
+        """Graphs of one decode step (one token per slot) reading the static
         buffer ``hidden [B, 1, hidden]``: returns a ``CapturedStep`` whose
         ``replay()`` appends a token to every slot and leaves the step's output
-        in ``out``.  Runs one step eagerly first (it sizes the buffers and
-        warms the libraries).  Replays do not advance the host length mirror:
+        in ``out``.  The step is two graphs, the page reservation and the
+        forward, so a caller can read the reservation's error bits between
+        them.  ``warm`` runs one step eagerly first (it sizes the buffers and
+        warms the libraries; without it the caller must have run a step of
+        this shape).  Replays do not advance the host length mirror:
         ``arena.sync_lengths()`` reads the device's."""
-        slots_d = torch.tensor([int(s) for s in slots], dtype=torch.int32, device=self.arena.device)
+        arena = self.arena
+        device = arena.device
+        slots_d = torch.tensor([int(s) for s in slots], dtype=torch.int32, device=device)
         widths_d = torch.ones_like(slots_d)
+        count = int(slots_d.numel())
         # the graph's split-K partials live in a workspace of its own, sized
         # for the waves fixed at capture and held by the CapturedStep
         spec = self.model.spec
-        waves = ops.default_waves(self.arena.fmt, spec.query_heads, 1, int(slots_d.numel()))
-        workspace = torch.empty(max(256, ops.workspace_bytes(self.arena.fmt, spec.query_heads, 1,
+        waves = ops.default_waves(arena.fmt, spec.query_heads, 1, count)
+        workspace = torch.empty(max(256, ops.workspace_bytes(arena.fmt, spec.query_heads, 1,
                                                              waves)),
-                                dtype=torch.uint8, device=self.arena.device)
-        res = self.arena.reserve(slots_d, widths_d)
-        self._forward(hidden, res, workspace, waves)
-        torch.cuda.synchronize(self.arena.device)
-        graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream(self.arena.device)
-        stream.wait_stream(torch.cuda.current_stream(self.arena.device))
+                                dtype=torch.uint8, device=device)
+        if warm:
+            res = arena.reserve(slots_d, widths_d)
+            self._forward(hidden, res, workspace, waves)
+        else:
+            res = Reservation(slots_d, widths_d,
+                              torch.empty((count, arena.max_pages), dtype=torch.int32,
+                                          device=device),
+                              torch.empty(count, dtype=torch.int32, device=device),
+                              torch.empty(count, dtype=torch.int32, device=device))
+        torch.cuda.synchronize(device)
+        reserve_graph, graph = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(stream):
+            with torch.cuda.graph(reserve_graph, stream=stream):
+                arena.reserve(slots_d, widths_d, out=res)
             with torch.cuda.graph(graph, stream=stream):
-                res_g = self.arena.reserve(slots_d, widths_d, out=res)
-                out = self._forward(hidden, res_g, workspace, waves)
-        torch.cuda.current_stream(self.arena.device).wait_stream(stream)
-        self.arena.sync_lengths()
-        return CapturedStep(graph, out, hidden, res, (slots_d, widths_d), workspace, waves)
+                out = self._forward(hidden, res, workspace, waves)
+        torch.cuda.current_stream(device).wait_stream(stream)
+        if warm:
+            arena.sync_lengths()
+        return CapturedStep(graph, out, hidden, res, (slots_d, widths_d), workspace, waves,
+                            reserve_graph)
 
 
 @dataclass
@@ -353,6 +372,9 @@ class CapturedStep:
     operands: tuple                 # slot ids and widths read by the reserve kernel
     workspace: torch.Tensor = None  # the attention's split-K partials (every layer's launch)
     waves: int = 0                  # the attention waves the workspace is sized for
+    reserve_graph: torch.cuda.CUDAGraph = None   # the page reservation, replayed first
 
     def replay(self):
+        if self.reserve_graph is not None:
+            self.reserve_graph.replay()
         self.graph.replay()

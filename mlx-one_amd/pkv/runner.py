@@ -67,10 +67,22 @@ class RunnerOutput:
 
 
 class PagedRunner:
-    def __init__(self, model, *, copy_on_write=False):
+    """``copy_on_write`` picks the transaction of host-bookkept caches (see the
+    module docstring).  Caches of a device arena (``CacheConfig(page_arena=
+    "device")``) always run as one ``DeviceRunner`` step, rolled back by
+    truncation; with ``graphs=True`` their repeated decode steps (the same
+    sequences, one token each) replay a captured HIP graph of the whole step."""
+
+    def __init__(self, model, *, copy_on_write=False, graphs=False):
         self.model = model
         self.copy_on_write = copy_on_write
+        self.graphs = graphs
         self.last_trace = {}
+        self._device_runners = {}
+        self._captured = {}            # (arena, slots) -> CapturedStep, oldest first
+        self.max_graphs = 8
+        self._last_signature = None
+        self._layouts = None
 
     def _validate(self, requests):
         """The reference's batch checks (``paged.py:308-345``), one pass per request."""
@@ -115,10 +127,153 @@ class PagedRunner:
             if r.runtime is not first.runtime:
                 raise ValueError("paged batch spans cache managers")
 
+    # -- device-arena batches -------------------------------------------------------------
+    def _validate_device(self, requests):
+        """The reference's batch checks for slot-backed caches: one arena, one
+        slot per request across its layers, layouts of the model."""
+        from pkv.device_cache import SlotLayerCache
+
+        first = requests[0]
+        layers = self.model.spec.layers
+        activation = self.model.activation_dtype
+        hidden = self.model.spec.hidden
+        arena = first.cache[0].arena
+        slots = set()
+        for r in requests:
+            caches = r.cache
+            if r.phase != first.phase or r.model_epoch != first.model_epoch \
+                    or len(caches) != len(layers):
+                raise ValueError("incompatible paged batch")
+            slot = caches[0].slot if isinstance(caches[0], SlotLayerCache) else None
+            for i, c in enumerate(caches):
+                if (not isinstance(c, SlotLayerCache) or c.slot != slot or c.layer_id != i
+                        or c.arena is not arena):
+                    raise ValueError("invalid paged layer mappings")
+                if c.dtype != activation:
+                    raise ModelCapabilityUnsupported("paged storage differs from execution precision")
+                lay = c.layout
+                if lay.num_kv_heads != layers[i].kv_heads or lay.head_dim != layers[i].key_dim:
+                    raise ValueError("paged layer layout differs from the model")
+            if slot in slots:
+                raise ValueError("a sequence appears twice in the batch")
+            slots.add(slot)
+            if r.handle is not None:
+                r.runtime._validate_handle(r.handle)
+                if r.handle.bundle.entries is not caches:
+                    raise ValueError("paged request does not own its cache mapping")
+            if int(r.hidden.shape[0]) < 1 or int(r.hidden.shape[-1]) != hidden:
+                raise ValueError("request hidden states do not match the model")
+            if r.runtime is not first.runtime:
+                raise ValueError("paged batch spans cache managers")
+        return arena
+
+    def _execute_device(self, requests):
+        import torch
+
+        from pkv.device_arena import DeviceRunner
+
+        # a batch of the same caches as the last one skips the per-layer
+        # checks (the caches of a handle never change); handles are re-checked
+        signature = tuple((id(r.cache), id(r.handle), r.phase, r.model_epoch) for r in requests)
+        if signature == self._last_signature and all(
+                r.handle is None or (not r.handle.closed and r.handle.bundle.entries is r.cache)
+                for r in requests) and all(
+                int(r.hidden.shape[-1]) == self.model.spec.hidden and int(r.hidden.shape[0]) >= 1
+                for r in requests):
+            arena = requests[0].cache[0].arena
+        else:
+            arena = self._validate_device(requests)
+            self._last_signature = signature
+        first = requests[0]
+        spec = self.model.spec
+        started = time.perf_counter()
+        widths = tuple(int(r.hidden.shape[0]) for r in requests)
+        width = max(widths)
+        slots = [r.cache[0].slot for r in requests]
+        runner = self._device_runners.get(id(arena))
+        if runner is None or runner.arena is not arena:
+            runner = self._device_runners[id(arena)] = DeviceRunner(self.model, arena)
+        transient = len(requests) * width * spec.num_layers * 4 * (
+            spec.hidden + (spec.query_heads + 2 * spec.kv_heads) * spec.head_dim) * 2
+        device = first.hidden.device
+        uniform = all(n == width for n in widths)
+        with ExitStack() as stack:
+            if first.runtime is not None:
+                stack.enter_context(first.runtime.transient_reservation(transient))
+            key = (id(arena), tuple(slots))
+            if self.graphs and width == 1 and uniform:
+                y = self._replay_decode(runner, key, slots, requests)
+            else:
+                if uniform:
+                    x = torch.stack([r.hidden for r in requests])
+                else:
+                    x = torch.zeros((len(requests), width, spec.hidden),
+                                    dtype=first.hidden.dtype, device=device)
+                    for i, r in enumerate(requests):
+                        x[i, :widths[i]] = r.hidden
+                y = runner.execute(slots, x, widths)
+        if uniform and not any(r.return_all_logits for r in requests):
+            outputs = y[:, width - 1:width].split(1)            # one call for every view
+        else:
+            outputs = []
+            for i, n in enumerate(widths):
+                begin = 0 if requests[i].return_all_logits else n - 1
+                outputs.append(y[i:i + 1, begin:n])
+        lengths = arena.lengths
+        for r in requests:
+            if r.handle is not None:
+                r.handle.token_count = lengths[r.cache[0].slot]
+        if self._layouts is None:
+            self._layouts = [vars(layer) for layer in spec.layers]
+        self.last_trace = {"direct_attention_calls": spec.num_layers,
+                           "kernel_version": KERNEL_VERSION, "phase": first.phase,
+                           "page_arena": "device", "graph_replay": bool(
+                               self.graphs and width == 1 and uniform),
+                           "slots": slots, "batch_size": len(requests),
+                           "real_tokens": sum(widths), "padded_tokens": len(requests) * width,
+                           "transient_reserved_bytes": transient,
+                           "layer_layouts": self._layouts,
+                           "duration_ms": (time.perf_counter() - started) * 1000}
+        return RunnerOutput(tuple(r.request_id for r in requests), tuple(outputs), widths)
+
+    def _replay_decode(self, runner, key, slots, requests):
+        """One decode step of ``slots`` as a graph replay (captured on first use
+        for this set of sequences; the capture runs the step eagerly).  The
+        reserve kernel's error bits are read before returning: a step that ran
+        out of pages raises ``CacheCapacityError`` and the slots stay as they
+        were (the failed reserve grew none of them)."""
+        import torch
+
+        arena = runner.arena
+        step = self._captured.get(key)
+        if step is None:
+            # this step runs eagerly (and checks itself); the next ones replay
+            x = torch.stack([r.hidden for r in requests])
+            y = runner.execute(slots, x, [1] * len(slots))
+            while len(self._captured) >= self.max_graphs:
+                self._captured.pop(next(iter(self._captured)))
+            self._captured[key] = runner.capture_decode(slots, x.clone(), warm=False)
+            return y
+        torch.stack([r.hidden for r in requests], out=step.hidden)
+        step.reserve_graph.replay()
+        probe = arena.error_probe()        # waits for the reservation only
+        step.graph.replay()
+        failed = arena.probe_failed(probe)
+        if failed:
+            # the failed reservation grew no slot; the forward appended nothing
+            arena._raise(failed)
+        for s in slots:
+            arena.lengths[s] += 1
+        return step.out.clone()
+
     def execute(self, requests):
         import torch
 
         requests = tuple(requests)
+        if not requests:
+            raise ValueError("empty paged batch")
+        if requests[0].cache and hasattr(requests[0].cache[0], "slot"):
+            return self._execute_device(requests)
         self._validate(requests)
         first = requests[0]
         spec = self.model.spec
