@@ -411,8 +411,9 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     }
   };
 
-  // query operands and row limits of the current piece
+  // query operands, row limits and per-row score scales of the current piece
   int lim[RB];
+  float rsc[RB];
   KT qv[RB][KB];
   KT qsl[SLOTS > 1 ? SLOTS : 1][KB];  // per slot: the lane's query operand in that slot's columns
   float qs[RB][NG];
@@ -428,6 +429,12 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       lim[rb] = live ? min(pos, t1 - 1) : -1;
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi) qs[rb][gi] = 0.0f;
+      // f16 operands hold at most 65504: a row of bf16 queries with a larger
+      // element (seen as a non-finite group sum) is converted again, scaled by
+      // a power of two sc that brings its largest element into [2^14, 2^15)
+      // (exact), and the inverse is folded into its softmax scale
+      float sc = 1.0f;
+      auto convert = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int d0 = 32 * kb + 8 * jj;
@@ -443,7 +450,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           float sum = 0.0f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const _Float16 hv = (_Float16)bits_to_float(e8[e], g.float_kind);
+            const _Float16 hv = (_Float16)(bits_to_float(e8[e], g.float_kind) * sc);
             v[e] = hv;
             sum += (float)hv;
           }
@@ -455,6 +462,38 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           qv[rb][kb] = __builtin_bit_cast(KT, packed);
         }
       }
+      };
+      convert();
+      if constexpr (QUANT) {
+        bool bad = false;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) bad |= !__builtin_isfinite(qs[rb][gi]);
+        if (__any(bad)) {  // rare: bf16 queries past the f16 range
+          float mx = 0.0f;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            const int d0 = 32 * kb + 8 * jj;
+            const u4 x = raw[rb][kb];
+            const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint16_t bits = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+              if (valid && d0 + e < g.dim) mx = fmaxf(mx, fabsf(bits_to_float(bits, g.float_kind)));
+            }
+          }
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          if (mx >= 32768.0f && mx < INFINITY) {
+            int ex;
+            frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+            sc = ldexpf(1.0f, 15 - ex);
+          }
+#pragma unroll
+          for (int gi = 0; gi < NG; ++gi) qs[rb][gi] = 0.0f;
+          convert();
+        }
+      }
+      rsc[rb] = a.scale_log2 / sc;
       if constexpr (QUANT) {
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
@@ -676,7 +715,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             v = acc[rb][0][r];
           }
           vis[rb][r] = my_ok && tok0 + r <= lim[rb];
-          v = vis[rb][r] ? v * a.scale_log2 : -INFINITY;
+          v = vis[rb][r] ? v * rsc[rb] : -INFINITY;
           s[rb][r] = v;
           need |= v > m[rb] + kTau;
         }

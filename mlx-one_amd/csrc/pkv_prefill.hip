@@ -110,6 +110,11 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];
   OT qv[RB][KB];
+  // f16 operands hold at most 65504: a row whose largest pre-scaled element
+  // reaches 2^15 is scaled by a power of two sc into [2^14, 2^15) (exact);
+  // its scores then leave the MFMA multiplied by sc, undone by isc
+  float sc[RB], isc[RB];
+  bool qscaled = false;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
@@ -120,6 +125,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     const int pos = a.q_pos ? a.q_pos[(int64_t)b * a.nq + qi] : L - width + qi;
     lim[rb] = live ? min(pos, L - 1) : -1;
     const uint16_t *qrow = a.q + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
+    float mx = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int d0 = 32 * kb + 8 * jj;
@@ -141,12 +147,39 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = bits_to_float(e8[e], g.float_kind) * a.scale_log2;
+        mx = fmaxf(mx, fabsf(x));
         if constexpr (F16) v[e] = (_Float16)x;
         else v[e] = (__bf16)x;
       }
       qv[rb][kb] = v;
     }
+    sc[rb] = isc[rb] = 1.0f;
+    if constexpr (F16) {
+      // the row's largest |q * scale * log2(e)| (lanes jj share the row);
+      // a scaled row converts again from memory (rare: huge queries only)
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (mx >= 32768.0f && mx < INFINITY) {
+        int ex;
+        frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+        sc[rb] = ldexpf(1.0f, 15 - ex);
+        isc[rb] = ldexpf(1.0f, ex - 15);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int d0 = 32 * kb + 8 * jj;
+          OT v;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint16_t bits = valid && d0 + e < g.dim ? qrow[d0 + e] : 0;
+            v[e] = (_Float16)(bits_to_float(bits, g.float_kind) * a.scale_log2 * sc[rb]);
+          }
+          qv[rb][kb] = v;
+        }
+      }
+    }
+    qscaled |= sc[rb] != 1.0f;
   }
+  qscaled = __any(qscaled);
 
   // ---- the block's visible span: tokens up to the largest limit; tiles
   // below the smallest live limit are seen whole by every live row
@@ -338,8 +371,9 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       mb[rb] = m[rb] == -INFINITY ? 0.0f : m[rb];
+      const float init = -mb[rb] * sc[rb];  // scaled rows: the MFMA sums carry sc
 #pragma unroll
-      for (int i = 0; i < 2; ++i) S[i][rb] = f4{-mb[rb], -mb[rb], -mb[rb], -mb[rb]};
+      for (int i = 0; i < 2; ++i) S[i][rb] = f4{init, init, init, init};
     }
     const uint16_t *kbase = img + 2 * pr * I::KTILE + col * I::KROW + 8 * jj;
 #pragma unroll
@@ -373,6 +407,10 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = S[i][rb][r];
+      if (qscaled) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[rb][e] *= isc[rb];
+      }
       if (!fast) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
