@@ -11,8 +11,10 @@ access pattern a 32-layer model has.  Inputs are synthetic and resident in HBM
 before timing.  The timed steps are captured as one HIP graph and replayed
 once untimed, then once timed for the step time (``--eager`` launches them
 from the host instead); ``roofline.achieved`` comes from HIP events around
-each attention launch in a host-launched pass over the same steps
-(``roofline.kernel_timing``).  Prints one JSON line (rank 0).
+each attention launch in a host-launched pass over the same steps, enqueued
+while a bounded spin kernel holds the stream so that no host latency sits
+between an event and its kernel (``roofline.kernel_timing``).  Prints one
+JSON line (rank 0).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
 """
@@ -34,6 +36,9 @@ for _p in (ROOT / "mlx-one_amd", ROOT):
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA (no sparsity)
+# GPU clock cycles the stream is held per step of the event pass (~100 us of
+# host enqueue time per step at ~2.4 GHz)
+SLEEP_CYCLES_PER_STEP = 240_000
 
 
 def measured_traffic(workload):
@@ -458,6 +463,9 @@ def main(argv=None):
     parser.add_argument("--waves", type=int, default=0,
                         help="attention work waves (0: the workload's partition size, else the "
                              "library default for the shape and batch)")
+    parser.add_argument("--decode-kernel", choices=("mfma", "valu"), default="mfma",
+                        help="kernel for decode rows (<= 4 query rows per KV head, quantized "
+                             "pages): the MFMA form (default) or the vector-ALU form")
     parser.add_argument("--graph", action="store_true",
                         help="layer workload: replay each decode step as a captured HIP graph "
                              "(the attention workloads replay their timed steps as one graph "
@@ -492,6 +500,7 @@ def main(argv=None):
     from pkv import _native, ops, workloads
 
     _native.load()
+    ops.select_decode_kernel(args.decode_kernel)
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     w = workloads.get(args.workload)
@@ -591,13 +600,19 @@ def main(argv=None):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     if graph is not None:
+        # Hold the stream with a bounded spin kernel while the host enqueues
+        # the pass, so that the events bracket GPU work only: a host slower
+        # than a short launch would otherwise leave its own latency between
+        # an event and the kernel behind it.
+        torch.cuda._sleep(int(args.steps * SLEEP_CYCLES_PER_STEP))
         for i in range(args.steps):
             step(args.warmup + i, events[i])
         torch.cuda.synchronize()
     attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
     ms_per_step = wall / args.steps * 1e3
     timing = ("HIP events per launch, host-launched pass over the timed steps after the "
-              "timed graph replay" if graph is not None else
+              "timed graph replay, enqueued behind a spin kernel (no host gaps)"
+              if graph is not None else
               "HIP events per launch in the timed host-launched steps")
     timed = plans[args.warmup:]
     mean_lens = np.mean([p[3] for p in timed], axis=0)
@@ -631,7 +646,9 @@ def main(argv=None):
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(w.name),
-                    "kernel": "pkv_paged_attention (attn_kernel + merge_kernel)",
+                    "kernel": "pkv_paged_attention ({} + merge_kernel)".format(
+                        "valu_kernel" if args.decode_kernel == "valu" and w.bits != 16 and
+                        w.num_queries * w.heads // w.kv_heads <= 4 else "attn_kernel"),
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if w.widths:
@@ -653,7 +670,8 @@ def main(argv=None):
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
                    "bits": w.bits, "group_size": w.group_size, "num_queries": w.num_queries,
                    "mean_context": float(mean_lens.mean()),
-                   "waves": waves, "layers_rotated": args.layers, "graph": graph is not None},
+                   "waves": waves, "layers_rotated": args.layers, "graph": graph is not None,
+                   "decode_kernel": args.decode_kernel},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
     }

@@ -151,6 +151,22 @@ int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const vo
                                 int32_t max_pages, const int32_t *seq_lens, const int32_t *q_pos,
                                 const int32_t *widths, float scale, int32_t waves, void *out);
 
+/*
+ * Which kernel serves decode rows -- at most 4 query rows per KV head
+ * (single-token decode at GQA <= 4) over quantized pages at head_dim <= 128:
+ * PKV_DECODE_MFMA (the default: score and value products on the matrix
+ * cores, queries in column slots) or PKV_DECODE_VALU (the same work split,
+ * partials and merge, with v_dot2_f32_f16 products on the vector ALU).
+ * Both compute the reference's result; they differ only in f32 summation
+ * order.  No counterpart in the reference (its Metal kernel has one form):
+ * kept so that the choice can be measured on the device.  Process-wide (read
+ * when a call launches); returns the previous choice, or
+ * PKV_INVALID_ARGUMENT.  Other shapes always run the MFMA kernels.
+ */
+#define PKV_DECODE_MFMA 0
+#define PKV_DECODE_VALU 1
+int pkv_select_decode_kernel(int kind);
+
 /* Waves the attention kernel keeps resident on the current device for this
  * layout and (num_heads, num_queries) (1 for query blocks served by the
  * prefill kernel).  <0 on error. */
@@ -158,8 +174,8 @@ int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t
 
 /* The `waves` pkv_paged_attention uses when given waves <= 0: the resident
  * waves, or half of them (one per SIMD) for decode rows (<= 4 query rows per
- * KV head) when the batch has at most a quarter as many (sequence, KV head)
- * segments as resident waves.  <0 on error. */
+ * KV head) on the MFMA decode kernel when the batch has at most a quarter as
+ * many (sequence, KV head) segments as resident waves.  <0 on error. */
 int32_t pkv_attention_default_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries,
                                     int32_t batch);
 

@@ -72,7 +72,8 @@ int cached_waves(const pkv_geometry &geo, int rows) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
   char key[128];
-  snprintf(key, sizeof key, "%d/%d/%d/%d/%d/%d", geo.hk, geo.dp, geo.bits, geo.group, geo.float_kind, rows);
+  snprintf(key, sizeof key, "%d/%d/%d/%d/%d/%d/%d", geo.hk, geo.dp, geo.bits, geo.group, geo.float_kind, rows,
+           pkv::decode_kernel());
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find({dev, key});
   if (it != cache.end()) return it->second;
@@ -139,6 +140,12 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
   return check_launch(pkv::launch_append((hipStream_t)stream, a), "append launch");
 }
 
+int pkv_select_decode_kernel(int kind) {
+  if (kind != PKV_DECODE_MFMA && kind != PKV_DECODE_VALU)
+    return fail(PKV_INVALID_ARGUMENT, "decode kernel must be PKV_DECODE_MFMA or PKV_DECODE_VALU");
+  return pkv::select_decode_kernel(kind);
+}
+
 int32_t pkv_attention_waves(const pkv_layout *layout, int32_t num_heads, int32_t num_queries) {
   pkv_geometry g;
   if (geometry(layout, &g) != PKV_OK) return -1;
@@ -164,8 +171,10 @@ int32_t pkv_attention_default_waves(const pkv_layout *layout, int32_t num_heads,
   // Decode rows (<= 4 per KV head: four tiles per iteration) of a batch with
   // few (sequence, KV head) segments: one wave per SIMD streams longer runs
   // with fewer pieces to merge and measures faster; with many segments, two
-  // waves per SIMD keep more of them in flight.
-  if (rows <= 4 && (int64_t)batch * g.hk * 4 <= resident) return std::max(1, resident / 2);
+  // waves per SIMD keep more of them in flight.  The VALU decode kernel
+  // (issue-bound: its waves cover each other's LDS permutes) keeps two.
+  const bool valu = pkv::decode_kernel() == pkv::kDecodeValu && g.bits != 16 && g.dp <= 128;
+  if (rows <= 4 && !valu && (int64_t)batch * g.hk * 4 <= resident) return std::max(1, resident / 2);
   return resident;
 }
 

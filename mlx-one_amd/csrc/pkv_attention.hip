@@ -48,6 +48,7 @@
 // pieces write (acc, m, l) partials that merge_kernel, launched next on the
 // same stream, combines by log-sum-exp (the kernel boundary makes them
 // visible across the XCDs' L2s without any cache maintenance in the loop).
+#include <atomic>
 #include <type_traits>
 
 #include "pkv_mfma.h"
@@ -948,6 +949,550 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 
 }
 
+// ---- VALU decode kernel --------------------------------------------------------
+//
+// The vector-ALU counterpart of attn_kernel for quantized pages, head_dim up
+// to 128 and at most 4 query rows per KV head (single-token decode at GQA <=
+// 4), chosen with pkv_select_decode_kernel.  The work split, pieces,
+// partials (combined by merge_kernel), page-id windows and load schedule are
+// attn_kernel's (two or four tiles per iteration); the products run as
+// v_dot2_f32_f16 over f16 pairs (codes as 1024 + c, f32 accumulation)
+// instead of MFMAs, with the same affine terms and the same f16 P'.
+//
+// Lane l = tok + 16*jj.  Scores: the K payload gives lane l token tok's
+// elements d = 32kb + 8jj + e; the lane dots them with all four query rows,
+// one sum per quantization group, and a butterfly over the jj lanes
+// (v_permlane32_swap, then v_permlane16_swap) leaves lane l with token tok's
+// sums for query row jj.  The 16 lanes of row jj share the row's running
+// max.  Values: the V payload gives lane l = col + 16*jj tokens 4jj..4jj+3 at
+// d = 16n + col; the lane fetches P' of those tokens for every row
+// (ds_bpermute of f16 pairs that neighbouring token lanes formed) and
+// accumulates O[row][d]; at the piece's end the same butterfly folds the jj
+// lanes' sums and leaves lane l row jj.
+template <int BITS, int DP, int G>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void valu_kernel(const AttnArgs a) {
+  using C = Cfg<BITS, DP, G, 1, 1, 4>;
+  constexpr int NG = C::NG, KB = C::KB, NB = C::NB, LW = C::LW;
+  // tiles per iteration: four at 4-bit with up to two groups per row, else
+  // two (payload and metadata registers of four tiles beside the four rows'
+  // query operands would spill)
+  constexpr int TPI = LW >= 8 || NG > 2 ? 2 : 4;
+  constexpr int R = 4;  // query rows per KV head, one per jj lane group
+  static_assert(BITS != 16 && DP <= 128, "VALU decode kernel: quantized pages, head_dim <= 128");
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  // Codes -> f16 pairs (1024 + c) as 32-bit words, the formulas of Conv<BITS>.
+  // Kept as plain words: built as a half vector and taken apart again before
+  // v_dot2, the high pair of a V word was dropped by this compiler (both
+  // products read the low pair).
+  auto kpairs = [](const uint32_t(&w)[LW], int kb, uint32_t(&o)[4]) __attribute__((always_inline)) {
+    if constexpr (BITS == 8) {
+      const uint32_t w0 = w[2 * kb], w1 = w[2 * kb + 1];
+      o[0] = perm(w0, kMagic, kSelLo); o[1] = perm(w0, kMagic, kSelHi);
+      o[2] = perm(w1, kMagic, kSelLo); o[3] = perm(w1, kMagic, kSelHi);
+    } else {
+      const uint32_t x = w[kb];
+      const uint32_t ev = x & 0x0F0F0F0Fu, od = (x >> 4) & 0x0F0F0F0Fu;
+      o[0] = perm(ev, kMagic, kNibLo); o[1] = perm(od, kMagic, kNibLo);
+      o[2] = perm(ev, kMagic, kNibHi); o[3] = perm(od, kMagic, kNibHi);
+    }
+  };
+  auto vpairs = [](const uint32_t(&w)[LW], int n, uint32_t &lo, uint32_t &hi) __attribute__((always_inline)) {
+    if constexpr (BITS == 8) {
+      lo = perm(w[n], kMagic, kSelLo);
+      hi = perm(w[n], kMagic, kSelHi);
+    } else {
+      const uint32_t x = w[n >> 1];
+      const uint32_t nb = (n & 1) ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
+      lo = perm(nb, kMagic, kNibLo);
+      hi = perm(nb, kMagic, kNibHi);
+    }
+  };
+
+  int lane = threadIdx.x;
+  int tok, jj;
+  auto refresh_lane = [&]() __attribute__((always_inline)) {
+    asm volatile("" : "+v"(lane));
+    tok = lane & 15;
+    jj = lane >> 4;
+  };
+  refresh_lane();
+  const int w = blockIdx.x;
+  const Geo &g = a.g;
+  const int hk = g.hk;
+  const int tpp_shift = __builtin_ctz(g.page / PKV_TILE);
+  const int tpp_mask = (1 << tpp_shift) - 1;
+
+  // ---- sequences and the split: as attn_kernel
+  int cbase = 0, len_l = 0, nt_l = 0, incl_l = 0, chunk_pre = 0, chunk_end = 0, lead = 0;
+  auto scan_chunk = [&](int base, int pre) __attribute__((always_inline)) {
+    cbase = base;
+    chunk_pre = pre;
+    incl_l = wave_scan_incl(base + lane < a.batch && nt_l > 0 ? nt_l + lead : 0, lane) + pre;
+    chunk_end = __builtin_amdgcn_readlane(incl_l, 63);
+  };
+  auto load_chunk = [&](int base, int pre) __attribute__((always_inline)) {
+    const int idx = base + lane;
+    len_l = idx < a.batch ? a.seq_lens[idx] : 0;
+    nt_l = idx < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, idx) : 0;
+    scan_chunk(base, pre);
+  };
+  len_l = lane < a.batch ? a.seq_lens[lane] : 0;
+  nt_l = lane < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, lane) : 0;
+  int all_tiles = wave_sum(nt_l), served = wave_sum(nt_l > 0 ? 1 : 0);
+  for (int c0 = 64; c0 < a.batch; c0 += 64) {
+    const int idx = c0 + lane;
+    const int nt = idx < a.batch ? split_tiles(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, idx) : 0;
+    all_tiles += wave_sum(nt);
+    served += wave_sum(nt > 0 ? 1 : 0);
+  }
+  const int t0 = __builtin_amdgcn_readfirstlane(all_tiles) * hk;
+  if (t0 == 0) return;
+  lead = charged_lead(a.seq_lens, a.widths, a.narrow_lo, a.narrow_q, a.batch, a.waves, a.lead, nt_l, t0, lane);
+  scan_chunk(0, 0);
+  const int T = t0 + __builtin_amdgcn_readfirstlane(served) * hk * lead;
+  const int W = min(a.waves, T);
+  if (w >= W) return;
+  Split sp;
+  sp.init(T, W);
+
+  auto locate = [&](int gt, int &pb, int &pkh, int &pL, int &pnt, int &pseg0)
+      __attribute__((always_inline)) {
+    if (gt < chunk_pre * hk) load_chunk(0, 0);
+    while (gt >= chunk_end * hk && cbase + 64 < a.batch) load_chunk(cbase + 64, chunk_end);
+    const unsigned long long hit = __ballot(cbase + lane < a.batch && incl_l * hk > gt);
+    const int f = hit ? __ffsll((long long)hit) - 1 : 0;
+    pb = cbase + f;
+    pnt = __builtin_amdgcn_readlane(nt_l, f);
+    pL = __builtin_amdgcn_readlane(len_l, f);
+    const int span = pnt + lead;
+    const int pre = (__builtin_amdgcn_readlane(incl_l, f) - span) * hk;
+    pkh = (gt - pre) / span;
+    pseg0 = pre + pkh * span;
+  };
+  auto fetch_window = [&](int pb, int win, int t1) __attribute__((always_inline)) -> int {
+    const int p = win + lane;
+    int id = -1;
+    if (p < a.max_pages && (int64_t)p * g.page < t1) id = a.table[(int64_t)pb * a.max_pages + p];
+    return id < a.num_pages ? id : -1;
+  };
+
+  // ---- query rows: every row's elements d = 32kb + 8jj + e, as raw words
+  // in the operand registers (converted in place by set_queries)
+  uint32_t qw[R][KB][4];  // plain words: see kpairs
+  auto fetch_row = [&](int pb, int pkh, int r) __attribute__((always_inline)) {
+    const int rowv = r < a.rows ? r : 0;  // rows past the block load row 0, zeroed later
+    const int qi = rowv / a.gqa, h = pkh * a.gqa + rowv % a.gqa;
+    const uint16_t *qrow = a.q + (((int64_t)pb * a.heads + h) * a.nq_stride + qi) * g.dim;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int d0 = 32 * kb + 8 * jj;
+      if ((g.dim & 7) == 0) {
+        const u4 x = *(const u4 *)(qrow + (d0 < g.dim ? d0 : 0));
+        qw[r][kb][0] = x.x; qw[r][kb][1] = x.y; qw[r][kb][2] = x.z; qw[r][kb][3] = x.w;
+      } else {
+        uint16_t e8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) e8[e] = qrow[d0 + e < g.dim ? d0 + e : 0];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) qw[r][kb][p] = (uint32_t)e8[2 * p] | ((uint32_t)e8[2 * p + 1] << 16);
+      }
+    }
+  };
+  auto fetch_q = [&](int pb, int pkh, int &qp) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) fetch_row(pb, pkh, r);
+    const int rj = jj < a.rows ? jj : 0;
+    qp = a.q_pos ? a.q_pos[(int64_t)pb * a.nq_stride + rj / a.gqa] : 0;
+  };
+
+  // f16 query operands of every row (in place); limit, group sums and score
+  // scale of the lane's row jj
+  int lim;
+  float rsc, qsj[NG];
+  auto set_queries = [&](int pb, int pkh, int pL, int pwidth, int t1, int qp) __attribute__((always_inline)) {
+    float rs[R], qs[R][NG];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool valid = r < a.rows;
+      // f16 operands hold at most 65504: a row of bf16 queries with a larger
+      // element (a non-finite group sum) is read and converted again, scaled
+      // by a power of two sc that brings its largest element into
+      // [2^14, 2^15) (exact), and the inverse is folded into its score scale
+      auto convert = [&](float sc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) qs[r][gi] = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int d0 = 32 * kb + 8 * jj;
+          const uint32_t w4[4] = {qw[r][kb][0], qw[r][kb][1], qw[r][kb][2], qw[r][kb][3]};
+          uint32_t o4[4];
+          float sum = 0.0f;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int e = 2 * p + h;
+              const uint16_t bits = (uint16_t)(w4[p] >> (16 * h));
+              const bool in = valid && d0 + e < g.dim;
+              const _Float16 hv = in ? (_Float16)(bits_to_float(bits, g.float_kind) * sc) : (_Float16)0.0f;
+              sum += (float)hv;
+              pair |= (uint32_t)__builtin_bit_cast(uint16_t, hv) << (16 * h);
+            }
+            o4[p] = pair;
+          }
+          qs[r][(32 * kb) / G] += sum;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) qw[r][kb][p] = o4[p];
+        }
+      };
+      convert(1.0f);
+      float sc = 1.0f;
+      bool bad = false;
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) bad |= !__builtin_isfinite(qs[r][gi]);
+      if (__any(bad)) {  // rare: bf16 queries past the f16 range
+        fetch_row(pb, pkh, r);
+        float mx = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int d0 = 32 * kb + 8 * jj;
+          const uint32_t w4[4] = {qw[r][kb][0], qw[r][kb][1], qw[r][kb][2], qw[r][kb][3]};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint16_t bits = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+            if (valid && d0 + e < g.dim) mx = fmaxf(mx, fabsf(bits_to_float(bits, g.float_kind)));
+          }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (mx >= 32768.0f && mx < INFINITY) {
+          int ex;
+          frexpf(mx, &ex);
+          sc = ldexpf(1.0f, 15 - ex);
+        }
+        convert(sc);
+      }
+      rs[r] = a.scale_log2 / sc;
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        qs[r][gi] += __shfl_xor(qs[r][gi], 16, 64);
+        qs[r][gi] += __shfl_xor(qs[r][gi], 32, 64);
+      }
+    }
+    // the lane's row jj
+    const int qi = jj / a.gqa;
+    const bool live = jj < a.rows && qi < pwidth;
+    const int pos = a.q_pos ? qp : pL - pwidth + qi;
+    lim = live ? min(pos, t1 - 1) : -1;
+    rsc = jj == 0 ? rs[0] : jj == 1 ? rs[1] : jj == 2 ? rs[2] : rs[3];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+      qsj[gi] = jj == 0 ? qs[0][gi] : jj == 1 ? qs[1][gi] : jj == 2 ? qs[2][gi] : qs[3][gi];
+  };
+
+  // rows r0..r3 summed over the jj lanes; lane l receives row jj's sum
+  auto fold_rows = [](float r0, float r1, float r2, float r3) __attribute__((always_inline)) -> float {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(r0), __float_as_uint(r2), false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(r1), __float_as_uint(r3), false, false);
+    const float a0 = __uint_as_float(x[0]) + __uint_as_float(x[1]);  // rows 0 | 2 (lanes < 32 | >= 32)
+    const float a1 = __uint_as_float(y[0]) + __uint_as_float(y[1]);  // rows 1 | 3
+    const auto z = __builtin_amdgcn_permlane16_swap(__float_as_uint(a0), __float_as_uint(a1), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);
+  };
+
+  // tiles of iteration `it` (as attn_kernel's plan)
+  auto plan = [&](int pta, int ntl, int pwin, int ppid, int it, int (&pg)[TPI], int (&tp)[TPI])
+      __attribute__((always_inline)) {
+    int mask = 0;
+#pragma unroll
+    for (int j = 0; j < TPI; ++j) {
+      const int tile = it * TPI + j;
+      int id = 0, t = 0;
+      if (tile < ntl) {
+        const int st = pta + tile;
+        const int pid_j = __builtin_amdgcn_readlane(ppid, (st >> tpp_shift) - pwin);
+        if (pid_j >= 0) {
+          id = pid_j;
+          t = st & tpp_mask;
+          mask |= 1 << j;
+        }
+      }
+      pg[j] = id;
+      tp[j] = t;
+    }
+    return mask;
+  };
+  auto head_at = [&](int pkh, int id) __attribute__((always_inline)) {
+    return a.pool + (int64_t)id * g.page_bytes + (int64_t)pkh * g.head_bytes;
+  };
+
+  uint32_t kw[TPI][LW], vw[TPI][LW];
+  uint32_t km[TPI][NG], vm[TPI][NG];  // the lane's token's (scale, bias) words per group
+  auto load_tok_meta = [&](uint32_t (&mw)[NG], const uint8_t *p) __attribute__((always_inline)) {
+    if constexpr (NG == 1) {
+      mw[0] = *(const uint32_t *)p;
+    } else if constexpr (NG == 2) {
+      const u2 x = *(const u2 *)p;
+      mw[0] = x.x; mw[1] = x.y;
+    } else {
+      const u4 x = *(const u4 *)p;
+      mw[0] = x.x; mw[1] = x.y; mw[2] = x.z; mw[3] = x.w;
+    }
+  };
+  auto load_k = [&](int pkh, const int (&pg)[TPI], const int (&tp)[TPI]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < TPI; ++j) {
+      const uint8_t *hb = head_at(pkh, pg[j]);
+      load_payload<C>(kw[j], hb + (int64_t)tp[j] * g.tile_bytes, lane);
+      load_tok_meta(km[j], hb + g.kmeta_offset + (int64_t)(tp[j] * PKV_TILE + tok) * (NG * 4));
+    }
+  };
+  auto load_v = [&](int pkh, const int (&pg)[TPI], const int (&tp)[TPI]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < TPI; ++j) {
+      const uint8_t *hb = head_at(pkh, pg[j]);
+      load_payload<C>(vw[j], hb + g.v_offset + (int64_t)tp[j] * g.tile_bytes, lane);
+      load_tok_meta(vm[j], hb + g.vmeta_offset + (int64_t)(tp[j] * PKV_TILE + tok) * (NG * 4));
+    }
+  };
+
+  // ---- pieces (as attn_kernel)
+  const int run_end = sp.start(w + 1);
+  int cb, ckh, cL, cnt, cseg0;
+  bool cfirst = true;
+  locate(sp.start(w), cb, ckh, cL, cnt, cseg0);
+  int cta = max(sp.start(w) - cseg0 - lead, 0);
+  int ctb = min(cnt, run_end - cseg0 - lead);
+  if (ctb <= 0) return;
+  int cpid = fetch_window(cb, cta >> tpp_shift, min(cL, ctb * PKV_TILE));
+
+  bool has_next = false;
+  int nb = 0, nkh = 0, nL = 0, nnt = 1, nta = 0, ntb = 0, npid = -1, nseg0 = 0;
+  auto set_next = [&](int gstart) __attribute__((always_inline)) {
+    locate(gstart, nb, nkh, nL, nnt, nseg0);
+    nta = max(gstart - nseg0 - lead, 0);
+    ntb = min(nnt, run_end - nseg0 - lead);
+    npid = fetch_window(nb, nta >> tpp_shift, min(nL, ntb * PKV_TILE));
+  };
+
+  int pg[TPI], npg[TPI], tp[TPI], ntp[TPI];
+
+  for (;;) {
+    refresh_lane();
+    const int width = a.widths ? a.widths[cb] : a.nq;
+    const int t0 = cta * PKV_TILE;
+    const int t1 = min(cL, ctb * PKV_TILE);
+    const int ntl = t1 > t0 ? (t1 - t0 + PKV_TILE - 1) / PKV_TILE : 0;
+    const int niters = max(1, (ntl + TPI - 1) / TPI);
+    int cwin = cta >> tpp_shift;
+    int cmask;
+    {
+      int qp;
+      fetch_q(cb, ckh, qp);
+      cmask = plan(cta, ntl, cwin, cpid, 0, pg, tp);
+      load_k(ckh, pg, tp);
+      load_v(ckh, pg, tp);
+      set_queries(cb, ckh, cL, width, t1, qp);
+      has_next = ctb == cnt && cseg0 + cnt + 2 * lead < run_end;
+      if (has_next) set_next(cseg0 + lead + cnt);
+    }
+    // P' pair sources: tokens 4jj, 4jj+1 (A) and 4jj+2, 4jj+3 (B) of row r sit
+    // in lanes 16r + 4jj and 16r + 4jj + 2 (byte addresses for ds_bpermute)
+    const int srcA = 4 * (4 * jj), srcB = 4 * (4 * jj + 2);
+
+    int cmask_next = 0;
+    float m = -INFINITY, lsum = 0.0f, corr[NG], osum[NG];
+    float O[R][NB];  // O[row][d = 16n + col], partial over the lane's tokens
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) { corr[gi] = 0.0f; osum[gi] = 0.0f; }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int n = 0; n < NB; ++n) O[r][n] = 0.0f;
+
+    auto iterate = [&](auto more, int it) __attribute__((always_inline)) {
+      constexpr bool MORE = decltype(more)::value;
+      refresh_lane();
+      // scores of the lane's token in each tile, row jj
+      float s[TPI];
+      bool vis[TPI];
+      bool need = false;
+#pragma unroll
+      for (int j = 0; j < TPI; ++j) {
+        s[j] = -INFINITY;
+        vis[j] = false;
+        if (cmask & (1 << j)) {
+          float acc[R][NG];
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) acc[r][gi] = 0.0f;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            uint32_t kx[4];
+            kpairs(kw[j], kb, kx);
+            const int gi = (32 * kb) / G;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              float t = acc[r][gi];
+#pragma unroll
+              for (int p = 0; p < 4; ++p)
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qw[r][kb][p]), __builtin_bit_cast(h2, kx[p]), t,
+                                           false);
+              acc[r][gi] = t;
+            }
+          }
+          float v;
+#pragma unroll
+          for (int gi = 0; gi < NG; ++gi) {
+            const float sg = fold_rows(acc[0][gi], acc[1][gi], acc[2][gi], acc[3][gi]);
+            const uint32_t word = km[j][gi];
+            const float ks = f16_bits_to_f32(word);
+            const float kbias = f16_bits_to_f32(word >> 16) - 1024.0f * ks;
+            const float term = ks * sg + qsj[gi] * kbias;
+            v = gi == 0 ? term : v + term;
+          }
+          vis[j] = t0 + (it * TPI + j) * PKV_TILE + tok <= lim;
+          s[j] = vis[j] ? v * rsc : -INFINITY;
+          need |= s[j] > m + kTau;
+        }
+      }
+      // K registers are free: request the next iteration's
+      if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int first = cta + (it + 1) * TPI;
+        const int last = cta + min((it + 1) * TPI + TPI, ntl) - 1;
+        if ((last >> tpp_shift) - cwin > 63) {
+          cwin = first >> tpp_shift;
+          cpid = fetch_window(cb, cwin, t1);
+        }
+        const int nmask = plan(cta, ntl, cwin, cpid, it + 1, npg, ntp);
+#pragma unroll
+        for (int j = 0; j < TPI; ++j) {
+          const uint8_t *hb = head_at(ckh, npg[j]);
+          load_payload<C>(kw[j], hb + (int64_t)ntp[j] * g.tile_bytes, lane);
+          load_tok_meta(km[j], hb + g.kmeta_offset + (int64_t)(ntp[j] * PKV_TILE + tok) * (NG * 4));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        cmask_next = nmask;
+      }
+      if (__any(need)) {
+        float tm = s[0];
+#pragma unroll
+        for (int j = 1; j < TPI; ++j) tm = fmaxf(tm, s[j]);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) tm = fmaxf(tm, __shfl_xor(tm, o, 64));
+        const float mn = fmaxf(m, tm);
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        lsum *= alpha;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) { corr[gi] *= alpha; osum[gi] *= alpha; }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float ar = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), 16 * r));
+#pragma unroll
+          for (int n = 0; n < NB; ++n) O[r][n] *= ar;
+        }
+      }
+      // probabilities, P' pairs and the bias terms of the lane's token
+      uint32_t pp[TPI][NG];
+#pragma unroll
+      for (int j = 0; j < TPI; ++j) {
+        const float p = vis[j] ? __builtin_amdgcn_exp2f(s[j] - m) : 0.0f;
+        lsum += p;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          const uint32_t word = vm[j][gi];
+          const _Float16 ps = vis[j] ? (_Float16)(p * f16_bits_to_f32(word)) : (_Float16)0.0f;
+          corr[gi] += vis[j] ? p * f16_bits_to_f32(word >> 16) : 0.0f;
+          osum[gi] += (float)ps;
+          const uint32_t own = __builtin_bit_cast(uint16_t, ps);
+          const uint32_t nbr = (uint32_t)__shfl_xor((int)own, 1, 64);
+          pp[j][gi] = own | (nbr << 16);  // (P'[tok], P'[tok + 1]) in even-tok lanes
+        }
+      }
+      // O[row][d] += P'[row][t] * (1024 + c[t][d]) over the lane's 4 tokens
+#pragma unroll
+      for (int j = 0; j < TPI; ++j) {
+        if (cmask & (1 << j)) {
+          uint32_t v01[NB], v23[NB];  // f16 pairs of tokens (4jj, 4jj+1) and (4jj+2, 4jj+3)
+#pragma unroll
+          for (int n = 0; n < NB; ++n) vpairs(vw[j], n, v01[n], v23[n]);
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+              const uint32_t pa = (uint32_t)__builtin_amdgcn_ds_bpermute(srcA + 64 * r, (int)pp[j][gi]);
+              const uint32_t pb = (uint32_t)__builtin_amdgcn_ds_bpermute(srcB + 64 * r, (int)pp[j][gi]);
+#pragma unroll
+              for (int n = 0; n < NB; ++n) {
+                if ((16 * n) / G != gi) continue;
+                float o = O[r][n];
+                o = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pa), __builtin_bit_cast(h2, v01[n]), o, false);
+                o = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pb), __builtin_bit_cast(h2, v23[n]), o, false);
+                O[r][n] = o;
+              }
+            }
+          }
+        }
+      }
+      // V registers are free: request the next iteration's
+      if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(ckh, npg, ntp);
+        __builtin_amdgcn_sched_barrier(0);
+        cmask = cmask_next;
+      }
+    };
+    for (int it = 0; it + 1 < niters; ++it) iterate(std::true_type(), it);
+    iterate(std::false_type(), niters - 1);
+
+    // ---- piece epilogue: row sums over the row's 16 token lanes, O folded
+    // over the jj lanes (lane l keeps row jj), output or partial
+    const bool whole = cta == 0 && ctb == cnt;
+    const int slot = cfirst ? 2 * w : 2 * w + 1;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      lsum += __shfl_xor(lsum, o, 64);
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        corr[gi] += __shfl_xor(corr[gi], o, 64);
+        osum[gi] += __shfl_xor(osum[gi], o, 64);
+      }
+    }
+    const int row = jj;
+    const bool writer = row < a.rows;
+    const int qi = row / a.gqa, h = ckh * a.gqa + row % a.gqa;
+    const float inv = 1.0f / fmaxf(lsum, 1e-20f);
+    uint16_t *o = a.out + (((int64_t)cb * a.heads + h) * a.nq_stride + qi) * g.dim;
+    float *pa = a.part_acc + ((int64_t)slot * a.rows + row) * DP;
+    float ov[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) ov[n] = fold_rows(O[0][n], O[1][n], O[2][n], O[3][n]);
+    if (writer) {
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const int gi = (16 * n) / G;
+        const float v = ov[n] + (corr[gi] - 1024.0f * osum[gi]);
+        const int d = 16 * n + tok;
+        if (whole) {
+          if (d < g.dim) o[d] = float_to_bits(v * inv, g.float_kind);
+        } else {
+          pa[d] = v;
+        }
+      }
+    }
+    if (writer && !whole && tok == 0)
+      *(float2 *)(a.part_ml + ((int64_t)slot * a.rows + row) * 2) = make_float2(m, lsum);
+
+    if (!has_next) break;
+    cb = nb; ckh = nkh; cL = nL; cnt = nnt; cseg0 = nseg0; cta = nta; ctb = ntb;
+    cfirst = false; cpid = npid;
+  }
+}
+
 // ---- host launcher ------------------------------------------------------------
 
 typedef void (*AttnKernel)(AttnArgs);
@@ -979,9 +1524,28 @@ static AttnKernel select_shape(const Geo &g) {
   return nullptr;
 }
 
+// The decode kernel for at most 4 rows per KV head over quantized pages at
+// head_dim <= 128: attn_kernel (MFMA, the default) or valu_kernel.
+static std::atomic<int> g_decode_kernel{kDecodeMfma};
+
+int select_decode_kernel(int kind) { return g_decode_kernel.exchange(kind); }
+int decode_kernel() { return g_decode_kernel.load(); }
+
+static AttnKernel select_valu(const Geo &g) {
+#define PKV_V(BITS_, DP_, G_) \
+  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return valu_kernel<BITS_, DP_, G_>;
+  PKV_V(8, 64, 32) PKV_V(8, 64, 64) PKV_V(8, 128, 32) PKV_V(8, 128, 64) PKV_V(8, 128, 128)
+  PKV_V(4, 64, 32) PKV_V(4, 64, 64) PKV_V(4, 128, 32) PKV_V(4, 128, 64) PKV_V(4, 128, 128)
+#undef PKV_V
+  return nullptr;
+}
+
 // Rows per KV head -> column slots: <= 4 rows: 4 slots, <= 8: 2, else 1
 // (two row blocks past 16 rows).
 static AttnKernel select_kernel(const Geo &g, int rows) {
+  if (rows <= 4 && g_decode_kernel.load() == kDecodeValu) {
+    if (const AttnKernel k = select_valu(g)) return k;
+  }
   if (rows <= 4) return select_shape<1, 4>(g);
   if (rows <= 8) return select_shape<1, 2>(g);
   if (rows <= 16) return select_shape<1, 1>(g);

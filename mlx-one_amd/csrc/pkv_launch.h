@@ -136,5 +136,10 @@ int attention_lead(const Geo &g, int rows);
 // Whether the split-K decode kernel serves this many rows per KV head (else
 // launch_prefill does, with no workspace and no merge).
 bool decode_serves(const Geo &g, int rows);
+// Decode kernel for <= 4 rows per KV head over quantized pages (head_dim <=
+// 128): process-wide; select returns the previous choice.
+constexpr int kDecodeMfma = 0, kDecodeValu = 1;
+int select_decode_kernel(int kind);
+int decode_kernel();
 
 }  // namespace pkv

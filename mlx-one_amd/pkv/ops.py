@@ -121,6 +121,22 @@ def attention_waves(fmt: PageFormat, num_heads, num_queries):
     return waves
 
 
+DECODE_KERNELS = {"mfma": 0, "valu": 1}
+
+
+def select_decode_kernel(kind):
+    """Choose the kernel for decode rows (at most 4 query rows per KV head over
+    quantized pages, head_dim <= 128): ``"mfma"`` (the default) or ``"valu"``
+    (the same split and merge with vector-ALU dot products).  Process-wide;
+    returns the previous choice."""
+    if kind not in DECODE_KERNELS:
+        raise ValueError(f"decode kernel must be one of {sorted(DECODE_KERNELS)}")
+    previous = int(nat.load().pkv_select_decode_kernel(DECODE_KERNELS[kind]))
+    if previous < 0:
+        nat.check(previous, "select decode kernel")
+    return {v: k for k, v in DECODE_KERNELS.items()}[previous]
+
+
 def default_waves(fmt: PageFormat, num_heads, num_queries, batch):
     """The waves ``paged_attention`` uses by default for this shape and batch."""
     waves = int(nat.load().pkv_attention_default_waves(fmt.c_layout, num_heads, num_queries,
