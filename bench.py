@@ -10,10 +10,11 @@ KV) so that a step never finds its KV in the 256 MB Infinity Cache, the same
 access pattern a 32-layer model has.  Inputs are synthetic and resident in HBM
 before timing.  The timed steps are captured as one HIP graph and replayed
 once untimed, then once timed for the step time (``--eager`` launches them
-from the host instead); ``roofline.achieved`` comes from HIP events around
-each attention launch in a host-launched pass over the same steps, enqueued
-while a bounded spin kernel holds the stream so that no host latency sits
-between an event and its kernel (``roofline.kernel_timing``).  Prints one
+from the host instead); ``roofline.achieved`` divides the algorithmic bytes
+(or flops) of a launch by its average duration: HIP events around a graph
+replay of the timed steps' attention launches, over the launch count
+(``roofline.kernel_timing``; events around each launch of a host-launched
+pass, which add their own overhead, are reported beside it).  Prints one
 JSON line (rank 0).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
@@ -532,11 +533,11 @@ def main(argv=None):
     lib = _native.load()
     layout = fmt.c_layout
 
-    def step(s, ev=None):
+    def step(s, ev=None, append=True):
         li, start, lens, _ = plans[s]
         layer = layers[li]
         h = _native.stream_handle(device)
-        if w.append_tokens:
+        if w.append_tokens and append:
             code = lib.pkv_append_quantize(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                            layer.new_k.data_ptr(), layer.new_v.data_ptr(), w.batch,
                                            w.append_tokens, layer.table.data_ptr(),
@@ -570,14 +571,17 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     # The timed steps are captured as one HIP graph and replayed (no host
-    # launch gaps): that replay gives the step time.  Events cannot be captured
-    # inside the graph on ROCm, so a host-launched pass over the same steps
-    # follows, with HIP events around each attention launch on its stream:
-    # that pass gives the launch duration for the roofline.  Re-running a step
+    # launch gaps): that replay gives the step time.  The attention launches
+    # of the same steps are captured as a second graph (no appends), replayed
+    # between two HIP events on the stream: that span over the launches gives
+    # the average launch duration for the roofline (kernel, merge and the gaps
+    # between them, as a graph-replayed decode loop runs them).  Events
+    # recorded around each launch of a host-launched pass are reported beside
+    # it; each such event adds its own few microseconds.  Re-running a step
     # re-appends the same token at the same position (idempotent).
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps)]
-    graph = None
+    graph = attn_graph = None
     if not args.eager:
         try:
             graph = torch.cuda.CUDAGraph()
@@ -585,11 +589,16 @@ def main(argv=None):
                 for i in range(args.steps):
                     step(args.warmup + i)
             graph.replay()          # untimed: the first replay uploads the graph
+            attn_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(attn_graph):
+                for i in range(args.steps):
+                    step(args.warmup + i, append=False)
+            attn_graph.replay()
             torch.cuda.synchronize()
         except RuntimeError as exc:
             print(f"bench: graph capture unavailable ({exc}); timing host launches",
                   file=sys.stderr)
-            graph = None
+            graph = attn_graph = None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     if graph is not None:
@@ -599,20 +608,25 @@ def main(argv=None):
             step(args.warmup + i, events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    span_ms = None
     if graph is not None:
+        span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        span[0].record(torch.cuda.current_stream(device))
+        attn_graph.replay()
+        span[1].record(torch.cuda.current_stream(device))
+        torch.cuda.synchronize()
+        span_ms = span[0].elapsed_time(span[1]) / args.steps
         # Hold the stream with a bounded spin kernel while the host enqueues
-        # the pass, so that the events bracket GPU work only: a host slower
-        # than a short launch would otherwise leave its own latency between
-        # an event and the kernel behind it.
+        # the per-launch pass, so that its events bracket GPU work only.
         torch.cuda._sleep(int(args.steps * SLEEP_CYCLES_PER_STEP))
         for i in range(args.steps):
             step(args.warmup + i, events[i])
         torch.cuda.synchronize()
-    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    per_launch_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+    attn_ms = span_ms if span_ms is not None else per_launch_ms
     ms_per_step = wall / args.steps * 1e3
-    timing = ("HIP events per launch, host-launched pass over the timed steps after the "
-              "timed graph replay, enqueued behind a spin kernel (no host gaps)"
-              if graph is not None else
+    timing = ("HIP events around a graph replay of the timed steps' attention launches, "
+              "divided by the launch count" if span_ms is not None else
               "HIP events per launch in the timed host-launched steps")
     timed = plans[args.warmup:]
     mean_lens = np.mean([p[3] for p in timed], axis=0)
@@ -651,6 +665,8 @@ def main(argv=None):
                         w.num_queries * w.heads // w.kv_heads <= 4 else "attn_kernel"),
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
+    if roofline is not None:
+        roofline["kernel_ms_events_per_launch"] = round(per_launch_ms, 5)
     if w.widths:
         metric = "mixed decode + prefill attention query tok/s (int8 paged KV, 1 layer)"
         unit = "tok/s"
