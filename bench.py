@@ -667,20 +667,23 @@ def main(argv=None):
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if roofline is not None:
         roofline["kernel_ms_events_per_launch"] = round(per_launch_ms, 5)
+    kv = {8: "int8", 4: "4-bit", 16: "bf16"}[w.bits]
+    shape = ("Llama-3-8B shape, " if (w.heads, w.kv_heads, w.head_dim) == (32, 8, 128) else "")
     if w.widths:
-        metric = "mixed decode + prefill attention query tok/s (int8 paged KV, 1 layer)"
+        metric = f"mixed decode + prefill attention query tok/s ({kv} paged KV, 1 layer)"
         unit = "tok/s"
     elif prefill:
-        metric = "chunked-prefill attention query tok/s (int8 paged KV, 1 layer)"
+        metric = f"chunked-prefill attention query tok/s ({kv} paged KV, 1 layer)"
         unit = "tok/s"
     else:
-        metric = "decode-attn seqs*tok/s (int8 paged KV, Llama-3-8B shape, 1 layer)"
+        kind = "decode-attn" if w.num_queries == 1 else f"verify-attn ({w.num_queries} drafts)"
+        metric = f"{kind} seqs*tok/s ({kv} paged KV, {shape}1 layer)"
         unit = "seqs*tok/s"
     result = {
         "metric": metric,
         "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8" if w.bits == 8 else f"u{w.bits}",
+        "scaling": "weak", "vs_baseline": None, "dtype": {8: "int8", 4: "u4", 16: "bf16"}[w.bits],
         "data": "synthetic",
         "config": {"workload": w.name, "batch": w.batch, "heads": w.heads,
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "page_tokens": w.page_tokens,
