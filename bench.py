@@ -13,9 +13,10 @@ once untimed, then once timed for the step time (``--eager`` launches them
 from the host instead); ``roofline.achieved`` divides the algorithmic bytes
 (or flops) of a launch by its average duration: HIP events around a graph
 replay of the timed steps' attention launches, over the launch count
-(``roofline.kernel_timing``; events around each launch of a host-launched
-pass, which add their own overhead, are reported beside it).  Prints one
-JSON line (rank 0).
+(``roofline.kernel_timing``; beside it: the launch inside the step, step
+graph time minus an append-only graph's, and events around each launch of a
+host-launched pass, which add their own overhead).  Prints one JSON line
+(rank 0).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
 """
@@ -533,7 +534,7 @@ def main(argv=None):
     lib = _native.load()
     layout = fmt.c_layout
 
-    def step(s, ev=None, append=True):
+    def step(s, ev=None, append=True, attend=True):
         li, start, lens, _ = plans[s]
         layer = layers[li]
         h = _native.stream_handle(device)
@@ -545,6 +546,8 @@ def main(argv=None):
                                            _native.ptr(layer.widths), None)
             if code:
                 _native.check(code, "append")
+        if not attend:
+            return
         if ev is not None:
             ev[0].record(torch.cuda.current_stream(device))
         code = lib.pkv_paged_attention(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
@@ -581,7 +584,7 @@ def main(argv=None):
     # re-appends the same token at the same position (idempotent).
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps)]
-    graph = attn_graph = None
+    graph = attn_graph = append_graph = None
     if not args.eager:
         try:
             graph = torch.cuda.CUDAGraph()
@@ -594,21 +597,30 @@ def main(argv=None):
                 for i in range(args.steps):
                     step(args.warmup + i, append=False)
             attn_graph.replay()
+            if w.append_tokens:
+                append_graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(append_graph):
+                    for i in range(args.steps):
+                        step(args.warmup + i, attend=False)
+                append_graph.replay()
             torch.cuda.synchronize()
         except RuntimeError as exc:
             print(f"bench: graph capture unavailable ({exc}); timing host launches",
                   file=sys.stderr)
-            graph = attn_graph = None
+            graph = attn_graph = append_graph = None
     torch.cuda.synchronize()
+    step_span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     t0 = time.perf_counter()
     if graph is not None:
+        step_span[0].record(torch.cuda.current_stream(device))
         graph.replay()
+        step_span[1].record(torch.cuda.current_stream(device))
     else:
         for i in range(args.steps):
             step(args.warmup + i, events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    span_ms = None
+    span_ms = append_ms = None
     if graph is not None:
         span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         span[0].record(torch.cuda.current_stream(device))
@@ -616,6 +628,12 @@ def main(argv=None):
         span[1].record(torch.cuda.current_stream(device))
         torch.cuda.synchronize()
         span_ms = span[0].elapsed_time(span[1]) / args.steps
+        if append_graph is not None:
+            span[0].record(torch.cuda.current_stream(device))
+            append_graph.replay()
+            span[1].record(torch.cuda.current_stream(device))
+            torch.cuda.synchronize()
+            append_ms = span[0].elapsed_time(span[1]) / args.steps
         # Hold the stream with a bounded spin kernel while the host enqueues
         # the per-launch pass, so that its events bracket GPU work only.
         torch.cuda._sleep(int(args.steps * SLEEP_CYCLES_PER_STEP))
@@ -667,6 +685,11 @@ def main(argv=None):
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if roofline is not None:
         roofline["kernel_ms_events_per_launch"] = round(per_launch_ms, 5)
+        if append_ms is not None:
+            # the launch inside the step (after its append): step graph time
+            # minus an append-only graph's
+            step_ms = step_span[0].elapsed_time(step_span[1]) / args.steps
+            roofline["kernel_ms_in_step"] = round(step_ms - append_ms, 5)
     kv = {8: "int8", 4: "4-bit", 16: "bf16"}[w.bits]
     shape = ("Llama-3-8B shape, " if (w.heads, w.kv_heads, w.head_dim) == (32, 8, 128) else "")
     if w.widths:
