@@ -465,6 +465,9 @@ def main(argv=None):
     parser.add_argument("--waves", type=int, default=0,
                         help="attention work waves (0: the workload's partition size, else the "
                              "library default for the shape and batch)")
+    parser.add_argument("--no-fuse", action="store_true",
+                        help="single-token steps: launch the append and the attention "
+                             "separately instead of the fused pkv_append_paged_attention")
     parser.add_argument("--decode-kernel", choices=("mfma", "valu"), default="mfma",
                         help="kernel for decode rows (<= 4 query rows per KV head, quantized "
                              "pages): the MFMA form (default) or the vector-ALU form")
@@ -534,10 +537,27 @@ def main(argv=None):
     lib = _native.load()
     layout = fmt.c_layout
 
+    # single-token steps append and attend in one call (pkv_append_paged_attention)
+    fused = (not args.no_fuse and w.append_tokens == 1 and w.num_queries == 1 and not w.widths
+             and args.decode_kernel == "mfma")
+
     def step(s, ev=None, append=True, attend=True):
         li, start, lens, _ = plans[s]
         layer = layers[li]
         h = _native.stream_handle(device)
+        if fused and append and attend:
+            if ev is not None:
+                ev[0].record(torch.cuda.current_stream(device))
+            code = lib.pkv_append_paged_attention(
+                h, layout, layer.pool.data_ptr(), layer.pool.shape[0], layer.new_k.data_ptr(),
+                layer.new_v.data_ptr(), layer.queries.data_ptr(), w.batch, w.heads,
+                layer.table.data_ptr(), layer.table.shape[1], lens.data_ptr(), scale, waves,
+                workspace.data_ptr(), workspace.numel(), layer.out.data_ptr())
+            if ev is not None:
+                ev[1].record(torch.cuda.current_stream(device))
+            if code:
+                _native.check(code, "append + attention")
+            return
         if w.append_tokens and append:
             code = lib.pkv_append_quantize(h, layout, layer.pool.data_ptr(), layer.pool.shape[0],
                                            layer.new_k.data_ptr(), layer.new_v.data_ptr(), w.batch,
@@ -595,9 +615,9 @@ def main(argv=None):
             attn_graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(attn_graph):
                 for i in range(args.steps):
-                    step(args.warmup + i, append=False)
+                    step(args.warmup + i, append=fused)   # fused: the step's one launch
             attn_graph.replay()
-            if w.append_tokens:
+            if w.append_tokens and not fused:
                 append_graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(append_graph):
                     for i in range(args.steps):
@@ -674,13 +694,18 @@ def main(argv=None):
                     "bytes_per_launch": int(attn_bytes),
                     "hbm_gbs": round(attn_bytes / (attn_ms / 1e3) / 1e9, 1)}
     elif attn_ms:
+        if fused:   # the launch also reads the new K/V rows
+            attn_bytes = step_bytes
         achieved = attn_bytes / (attn_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(w.name),
-                    "kernel": "pkv_paged_attention ({} + merge_kernel)".format(
-                        "valu_kernel" if args.decode_kernel == "valu" and w.bits != 16 and
-                        w.num_queries * w.heads // w.kv_heads <= 4 else "attn_kernel"),
+                    "kernel": ("pkv_append_paged_attention (attn_kernel with the fused "
+                               "append + merge_kernel)" if fused else
+                               "pkv_paged_attention ({} + merge_kernel)".format(
+                                   "valu_kernel" if args.decode_kernel == "valu" and
+                                   w.bits != 16 and w.num_queries * w.heads // w.kv_heads <= 4
+                                   else "attn_kernel")),
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if roofline is not None:
@@ -713,7 +738,7 @@ def main(argv=None):
                    "bits": w.bits, "group_size": w.group_size, "num_queries": w.num_queries,
                    "mean_context": float(mean_lens.mean()),
                    "waves": waves, "layers_rotated": args.layers, "graph": graph is not None,
-                   "decode_kernel": args.decode_kernel},
+                   "decode_kernel": args.decode_kernel, "fused_append": fused},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
     }

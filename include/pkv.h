@@ -129,6 +129,30 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
                         int64_t workspace_bytes, void *out);
 
 /*
+ * One single-token step: append the new K/V token of every sequence (as
+ * pkv_append_quantize with tokens = 1 at position seq_lens[b] - 1) and
+ * attend its one query (as pkv_paged_attention with num_queries = 1, q_pos
+ * NULL, widths NULL), in one launch where the decode kernel serves the shape
+ * (quantized pages, at most 8 query rows per KV head): the wave that attends
+ * a sequence's last tile quantizes the new token, stores it and uses it.
+ * Other shapes run the append and the attention as two launches.  Replaces
+ * the append-then-attend pair of PagedBatchCache.attend (engine/paged.py:
+ * 260-263) for a decode step; pages and output equal the two separate calls'
+ * bit for bit.
+ *
+ *  pool         : writable (the new tokens land in it)
+ *  keys, values : [batch][HK][1][head_dim], float_kind
+ *  seq_lens     : [batch] tokens in each sequence after the append (>= 1)
+ *  other arguments as pkv_paged_attention (queries [batch][num_heads][1][head_dim])
+ */
+int pkv_append_paged_attention(void *stream, const pkv_layout *layout, void *pool,
+                               int64_t num_pages, const void *keys, const void *values,
+                               const void *queries, int32_t batch, int32_t num_heads,
+                               const int32_t *block_table, int32_t max_pages,
+                               const int32_t *seq_lens, float scale, int32_t waves,
+                               void *workspace, int64_t workspace_bytes, void *out);
+
+/*
  * pkv_paged_attention without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference (its

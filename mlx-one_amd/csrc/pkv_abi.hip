@@ -135,6 +135,7 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
   a.max_pages = max_pages;
   a.table = block_table;
   a.start_pos = start_pos;
+  a.lens_after = nullptr;
   a.widths = widths;
   a.new_lens = new_lens;
   return check_launch(pkv::launch_append((hipStream_t)stream, a), "append launch");
@@ -201,11 +202,18 @@ namespace {
 // The attention entry points' common body.  `fit_waves`: when the caller
 // leaves the waves to the library, use no more than the workspace holds
 // partials for (the split is correct at any wave count).
+// The new token of every sequence, for pkv_append_paged_attention.
+struct FusedAppend {
+  void *pool;
+  const void *keys, *values;  // [batch][HK][1][dim]
+};
+
 int paged_attention_impl(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
                          const void *queries, int32_t batch, int32_t num_heads, int32_t num_queries,
                          const int32_t *block_table, int32_t max_pages, const int32_t *seq_lens,
                          const int32_t *q_pos, const int32_t *widths, float scale, int32_t waves,
-                         void *workspace, int64_t workspace_bytes, void *out, bool fit_waves) {
+                         void *workspace, int64_t workspace_bytes, void *out, bool fit_waves,
+                         const FusedAppend *fused = nullptr) {
   pkv_geometry geo;
   if (int rc = geometry(layout, &geo)) return rc;
   if (batch < 0) return fail(PKV_INVALID_ARGUMENT, "negative batch");
@@ -274,6 +282,31 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     }
   }
 
+  // The fused append: in the decode kernel when it serves the shape, else
+  // one append launch ahead of the attention.
+  if (fused) {
+    if (!fused->keys || !fused->values)
+      return fail(PKV_INVALID_ARGUMENT, "fused append requires the new keys and values");
+    if (wide || !pkv::append_fusable(pkv::to_geo(geo), rows)) {
+      pkv::AppendArgs ap;
+      ap.g = pkv::to_geo(geo);
+      ap.pool = (uint8_t *)fused->pool;
+      ap.num_pages = num_pages;
+      ap.keys = (const uint16_t *)fused->keys;
+      ap.values = (const uint16_t *)fused->values;
+      ap.batch = batch;
+      ap.tokens = 1;
+      ap.max_pages = max_pages;
+      ap.table = block_table;
+      ap.start_pos = nullptr;
+      ap.widths = nullptr;
+      ap.lens_after = seq_lens;
+      ap.new_lens = nullptr;
+      if (int rc = check_launch(pkv::launch_append((hipStream_t)stream, ap), "append launch")) return rc;
+      fused = nullptr;
+    }
+  }
+
   pkv::AttnArgs a;
   a.g = pkv::to_geo(geo);
   a.pool = (const uint8_t *)pool;
@@ -313,6 +346,11 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     a.lead = pkv::attention_lead(a.g, a.rows);
     a.part_ml = (float *)((char *)workspace + t.ws.ml);
     a.part_acc = (float *)((char *)workspace + t.ws.acc);
+    if (fused) {
+      a.wpool = (uint8_t *)fused->pool;
+      a.new_k = (const uint16_t *)fused->keys;
+      a.new_v = (const uint16_t *)fused->values;
+    }
     if (int rc = check_launch(pkv::launch_attention((hipStream_t)stream, a), "attention launch"))
       return rc;
     pkv::MergeArgs m;
@@ -389,6 +427,17 @@ int pkv_paged_attention(void *stream, const pkv_layout *layout, const void *pool
   return paged_attention_impl(stream, layout, pool, num_pages, queries, batch, num_heads,
                               num_queries, block_table, max_pages, seq_lens, q_pos, widths, scale,
                               waves, workspace, workspace_bytes, out, false);
+}
+
+int pkv_append_paged_attention(void *stream, const pkv_layout *layout, void *pool, int64_t num_pages,
+                               const void *keys, const void *values, const void *queries,
+                               int32_t batch, int32_t num_heads, const int32_t *block_table,
+                               int32_t max_pages, const int32_t *seq_lens, float scale,
+                               int32_t waves, void *workspace, int64_t workspace_bytes, void *out) {
+  const FusedAppend fused{pool, keys, values};
+  return paged_attention_impl(stream, layout, pool, num_pages, queries, batch, num_heads, 1,
+                              block_table, max_pages, seq_lens, nullptr, nullptr, scale, waves,
+                              workspace, workspace_bytes, out, false, &fused);
 }
 
 int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const void *pool,

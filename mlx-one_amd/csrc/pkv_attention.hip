@@ -52,6 +52,7 @@
 #include <type_traits>
 
 #include "pkv_mfma.h"
+#include "pkv_token.h"
 
 namespace pkv {
 
@@ -297,12 +298,13 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
   }
 }
 
-template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS, bool APPEND>
 __global__ __launch_bounds__(64)
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS)))) void attn_kernel(
     const AttnArgs a) {
   using C = Cfg<BITS, DP, G, RB, FK, SLOTS>;
   constexpr bool QUANT = C::QUANT;
+  static_assert(!APPEND || (QUANT && RB == 1), "fused append: quantized pages, one row block");
   constexpr int NG = C::NG, KB = C::KB, NB = C::NB, RPS = C::RPS;
   // MFMA operand types: quantized pages run in f16 (codes as 1024 + c).
   using FO = FloatOps<QUANT ? 1 : FK>;
@@ -600,6 +602,122 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 
   int pg[SLOTS], npg[SLOTS], tp[SLOTS], ntp[SLOTS];
 
+  // ---- fused single-token append (APPEND).  The wave whose piece holds a
+  // segment's last tile quantizes the sequence's new K/V token (it sits at
+  // seq_lens - 1) into LDS, stores it into its page slot, and patches its
+  // codes and (scale, bias) words into the tile registers of the iteration
+  // that holds it; no other wave reads that tile in this launch, so the
+  // store needs no ordering against the tile loads.
+  __shared__ uint8_t s_app_codes[2][APPEND ? DP : 4];
+  __shared__ uint32_t s_app_meta[2][8];
+  int app_it = -1, app_j = 0, app_tt = 0;
+  // the new rows are requested with the piece's queries, ahead of its tiles
+  // (loads return in order)
+  constexpr int AEPL = DP / 64;
+  uint16_t app_raw[APPEND ? 2 : 1][APPEND ? AEPL : 1];
+  int app_pid = -1;
+  auto append_fetch = [&](int pb, int pkh, int pos) __attribute__((always_inline)) {
+    if constexpr (APPEND) {
+      app_pid = a.table[(int64_t)pb * a.max_pages + pos / g.page];
+      const int64_t row = ((int64_t)pb * hk + pkh) * g.dim;
+#pragma unroll
+      for (int side = 0; side < 2; ++side) {
+        const uint16_t *src = (side ? a.new_v : a.new_k) + row;
+#pragma unroll
+        for (int i = 0; i < AEPL; ++i) {
+          const int d = lane * AEPL + i;
+          app_raw[side][i] = d < g.dim ? src[d] : (uint16_t)0;
+        }
+      }
+    }
+  };
+  auto append_token = [&](int pkh, int pos, int pta) __attribute__((always_inline)) {
+    if constexpr (APPEND) {
+      if (app_pid < 0 || app_pid >= a.num_pages) return;  // an unmapped page holds no tile either
+#pragma unroll
+      for (int side = 0; side < 2; ++side) {
+        float x[AEPL];
+#pragma unroll
+        for (int i = 0; i < AEPL; ++i) {
+          const int d = lane * AEPL + i;
+          x[i] = d < g.dim ? bits_to_float(app_raw[side][i], g.float_kind) : 0.0f;  // zero pad
+        }
+        quantize_row<AEPL>(x, lane, G, BITS, s_app_codes[side], s_app_meta[side]);
+      }
+      wave_lds_sync();
+      store_token<DP, BITS>(g, a.wpool + (int64_t)app_pid * g.page_bytes + (int64_t)pkh * g.head_bytes,
+                            pos % g.page, s_app_codes[0], s_app_codes[1], s_app_meta[0], s_app_meta[1],
+                            lane);
+      const int tile = pos / PKV_TILE - pta;  // within the piece
+      app_it = tile / SLOTS;
+      app_j = tile % SLOTS;
+      app_tt = pos % PKV_TILE;
+    }
+  };
+  // the token's K payload (lanes col == tt hold its elements d = 32kb + 8jj + e)
+  // and K meta word (lanes of its slot whose four tokens 4jj..4jj+3 hold it)
+  auto patch_k = [&]() __attribute__((always_inline)) {
+    if constexpr (APPEND) {
+      const bool mine = col == app_tt;
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j) {
+        if (j != app_j) continue;
+#pragma unroll
+        for (int x = 0; x < C::LW; ++x) {
+          uint32_t word = 0;
+          if constexpr (BITS == 8) {
+            word = *(const uint32_t *)&s_app_codes[0][32 * (x / 2) + 8 * jj + 4 * (x % 2)];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              word |= (uint32_t)(s_app_codes[0][32 * x + 8 * jj + e] & 15) << (4 * k4_nibble(e));
+          }
+          kw[j][x] = mine ? word : kw[j][x];
+        }
+      }
+      const bool mm = slot_l == app_j && jj == app_tt / 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+          if (r == app_tt % 4) km[r * NG + gi] = mm ? s_app_meta[0][gi] : km[r * NG + gi];
+    }
+  };
+  // the token's V payload (lanes jj == tt/4, byte r = tt%4 of each block) and V meta word
+  auto patch_v = [&]() __attribute__((always_inline)) {
+    if constexpr (APPEND) {
+      const int r = app_tt % 4;
+      const bool mine = jj == app_tt / 4;
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j) {
+        if (j != app_j) continue;
+        if constexpr (BITS == 8) {
+#pragma unroll
+          for (int n = 0; n < NB; ++n) {
+            const uint32_t sh = 8 * r;
+            const uint32_t word = (vw[j][n] & ~(0xFFu << sh)) | ((uint32_t)s_app_codes[1][16 * n + col] << sh);
+            vw[j][n] = mine ? word : vw[j][n];
+          }
+        } else {
+#pragma unroll
+          for (int m2 = 0; m2 < NB / 2; ++m2) {
+            const uint32_t sh = 8 * v4_byte(r);
+            const uint32_t byte = (uint32_t)(s_app_codes[1][32 * m2 + col] & 15) |
+                                  ((uint32_t)(s_app_codes[1][32 * m2 + 16 + col] & 15) << 4);
+            const uint32_t word = (vw[j][m2] & ~(0xFFu << sh)) | (byte << sh);
+            vw[j][m2] = mine ? word : vw[j][m2];
+          }
+        }
+      }
+      const bool mm = slot_l == app_j && jj == app_tt / 4;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+          if (rr == r) vm[rr * NG + gi] = mm ? s_app_meta[1][gi] : vm[rr * NG + gi];
+    }
+  };
+
   for (;;) {
     refresh_lane();
     // ---- start the piece: query rows and its first tiles, in flight together
@@ -610,14 +728,25 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     const int niters = max(1, (ntl + SLOTS - 1) / SLOTS);
     int cwin = cta >> tpp_shift;
     int cmask;
+    const bool appends = APPEND && ctb == cnt && cL > 0;  // the piece holds the segment's last tile
     {
       u4 raw[RB][KB];
       int qp[RB];
+      if constexpr (APPEND) {
+        if (appends) append_fetch(cb, ckh, cL - 1);
+      }
       fetch_q(cb, ckh, raw, qp);
       cmask = plan(cta, ntl, cwin, cpid, 0, pg, tp);
       load_k(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.kmeta_offset));
       load_v(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.vmeta_offset));
       set_queries(cL, width, t1, raw, qp);
+      // the new token: quantized and stored while the piece's first tiles
+      // are in flight (it is patched into the registers of the piece's last
+      // iteration)
+      if constexpr (APPEND) {
+        app_it = -1;
+        if (appends) append_token(ckh, cL - 1, cta);
+      }
       // the rest of the run is the next piece: its page-id window now
       has_next = ctb == cnt && cseg0 + cnt + 2 * lead < run_end;
       if (has_next) set_next(cseg0 + lead + cnt);
@@ -652,6 +781,11 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     auto iterate = [&](auto more, int it) __attribute__((always_inline)) {
       constexpr bool MORE = decltype(more)::value;
       refresh_lane();
+      // the appended token sits in the piece's last tile, hence in its last
+      // iteration (the peeled one): the loop body stays the plain kernel's
+      if constexpr (APPEND && !MORE) {
+        if (app_it >= 0) patch_k();
+      }
       // Float pages: a page reused after another sequence may hold anything
       // past this piece's last token, and the column-slot products multiply
       // a slot's K rows by other slots' zero query columns (and every V row by
@@ -760,6 +894,9 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
           for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
+      }
+      if constexpr (APPEND && !MORE) {
+        if (app_it >= 0) patch_v();
       }
       // probabilities and the P operands (per group for quantized V).  Masked
       // tokens contribute exact zeros through selects, whatever their page
@@ -1497,19 +1634,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void va
 
 typedef void (*AttnKernel)(AttnArgs);
 
-template <int BITS, int DP, int G, int RB, int FK, int SLOTS>
+template <int BITS, int DP, int G, int RB, int FK, int SLOTS, bool APPEND>
 static AttnKernel kernel_of() {
   if constexpr (RB > 1 && DP > 128) {
     return nullptr;  // 17..32 rows at head_dim > 128 run on the prefill kernel
+  } else if constexpr (APPEND && (BITS == 16 || RB > 1)) {
+    return nullptr;  // the fused append serves quantized pages at one row block
   } else {
-    return attn_kernel<BITS, DP, G, RB, FK, fit_slots(BITS, DP, G, SLOTS)>;
+    return attn_kernel<BITS, DP, G, RB, FK, fit_slots(BITS, DP, G, SLOTS), APPEND>;
   }
 }
 
-template <int RB, int SLOTS>
+template <int RB, int SLOTS, bool APPEND = false>
 static AttnKernel select_shape(const Geo &g) {
 #define PKV_Q(BITS_, DP_, G_) \
-  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return kernel_of<BITS_, DP_, G_, RB, 1, SLOTS>();
+  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return kernel_of<BITS_, DP_, G_, RB, 1, SLOTS, APPEND>();
   PKV_Q(8, 64, 32) PKV_Q(8, 64, 64)
   PKV_Q(8, 128, 32) PKV_Q(8, 128, 64) PKV_Q(8, 128, 128)
   PKV_Q(8, 256, 32) PKV_Q(8, 256, 64) PKV_Q(8, 256, 128)
@@ -1518,7 +1657,7 @@ static AttnKernel select_shape(const Geo &g) {
   PKV_Q(4, 256, 32) PKV_Q(4, 256, 64) PKV_Q(4, 256, 128)
 #undef PKV_Q
 #define PKV_F(DP_, FK_) \
-  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_) return kernel_of<16, DP_, 32, RB, FK_, SLOTS>();
+  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_) return kernel_of<16, DP_, 32, RB, FK_, SLOTS, false>();
   PKV_F(64, 0) PKV_F(64, 1) PKV_F(128, 0) PKV_F(128, 1) PKV_F(256, 0) PKV_F(256, 1)
 #undef PKV_F
   return nullptr;
@@ -1541,8 +1680,15 @@ static AttnKernel select_valu(const Geo &g) {
 }
 
 // Rows per KV head -> column slots: <= 4 rows: 4 slots, <= 8: 2, else 1
-// (two row blocks past 16 rows).
-static AttnKernel select_kernel(const Geo &g, int rows) {
+// (two row blocks past 16 rows).  With the fused single-token append: the
+// MFMA kernels of up to 8 rows over quantized pages (else none).
+static AttnKernel select_kernel(const Geo &g, int rows, bool append = false) {
+  if (append) {
+    if (g.bits == 16) return nullptr;
+    if (rows <= 4) return select_shape<1, 4, true>(g);
+    if (rows <= 8) return select_shape<1, 2, true>(g);
+    return nullptr;
+  }
   if (rows <= 4 && g_decode_kernel.load() == kDecodeValu) {
     if (const AttnKernel k = select_valu(g)) return k;
   }
@@ -1554,6 +1700,8 @@ static AttnKernel select_kernel(const Geo &g, int rows) {
 }
 
 bool decode_serves(const Geo &g, int rows) { return select_kernel(g, rows) != nullptr; }
+
+bool append_fusable(const Geo &g, int rows) { return select_kernel(g, rows, true) != nullptr; }
 
 int attention_waves(const Geo &g, int rows) {
   const AttnKernel k = select_kernel(g, rows);
@@ -1575,7 +1723,7 @@ int attention_waves(const Geo &g, int rows) {
 int attention_lead(const Geo &, int) { return 8; }
 
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
-  const AttnKernel k = select_kernel(a.g, a.rows);
+  const AttnKernel k = select_kernel(a.g, a.rows, a.new_k != nullptr);
   if (!k) return hipErrorInvalidValue;
   if (a.waves <= 0) return hipSuccess;
   hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64), 0, stream, a);

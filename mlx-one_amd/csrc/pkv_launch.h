@@ -11,6 +11,7 @@ struct AppendArgs {
   const uint16_t *keys, *values;  // [B][HK][T][D]
   int batch, tokens, max_pages;
   const int32_t *table, *start_pos, *widths;
+  const int32_t *lens_after;  // start_pos NULL: start = lens_after[b] - tokens
   int32_t *new_lens;
 };
 
@@ -53,6 +54,11 @@ struct AttnArgs {
   float *part_acc;   // [2*waves][rows][DP]
   float *part_ml;    // [2*waves][rows][2]
   uint16_t *out;     // [B][H][Q][D]
+  // Fused single-token append (new_k non-NULL): each sequence's new K/V row
+  // [B][HK][D] is quantized into slot seq_lens[b] - 1 of its pages (wpool is
+  // the pool, writable) by the wave that attends the sequence's last tile.
+  uint8_t *wpool = nullptr;
+  const uint16_t *new_k = nullptr, *new_v = nullptr;
 };
 
 struct MergeArgs {
@@ -136,6 +142,9 @@ int attention_lead(const Geo &g, int rows);
 // Whether the split-K decode kernel serves this many rows per KV head (else
 // launch_prefill does, with no workspace and no merge).
 bool decode_serves(const Geo &g, int rows);
+// Whether the decode kernel fuses the single-token append for this layout and
+// row count (quantized pages, at most 8 rows per KV head).
+bool append_fusable(const Geo &g, int rows);
 // Decode kernel for <= 4 rows per KV head over quantized pages (head_dim <=
 // 128): process-wide; select returns the previous choice.
 constexpr int kDecodeMfma = 0, kDecodeValu = 1;

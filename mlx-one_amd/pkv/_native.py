@@ -40,6 +40,8 @@ SIGNATURES = {
                              _c_p, _c_p, _f32, _i32, _c_p, _i64, _c_p], ctypes.c_int),
     "pkv_paged_attention_noalloc": ([_c_p, _LP, _c_p, _i64, _c_p, _i32, _i32, _i32, _c_p, _i32,
                                      _c_p, _c_p, _c_p, _f32, _i32, _c_p], ctypes.c_int),
+    "pkv_append_paged_attention": ([_c_p, _LP, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _c_p,
+                                    _i32, _c_p, _f32, _i32, _c_p, _i64, _c_p], ctypes.c_int),
     "pkv_select_decode_kernel": ([ctypes.c_int], ctypes.c_int),
     "pkv_attention_waves": ([_LP, _i32, _i32], _i32),
     "pkv_attention_default_waves": ([_LP, _i32, _i32, _i32], _i32),

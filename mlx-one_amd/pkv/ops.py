@@ -226,6 +226,53 @@ def paged_attention(fmt: PageFormat, pool, queries, block_table, seq_lens, *, sc
     return out
 
 
+def append_paged_attention(fmt: PageFormat, pool, keys, values, queries, block_table, seq_lens, *,
+                           scale, waves=0, workspace=None, out=None):
+    """One single-token step: append ``keys``/``values [B, HK, 1, D]`` at
+    position ``seq_lens - 1`` (``seq_lens`` counts the tokens after the
+    append) and attend ``queries [B, H, 1, D]`` -- one launch where the decode
+    kernel serves the shape (quantized pages, at most 8 query rows per KV
+    head), else an append launch and the attention.  Pages and output equal
+    ``append_quantize`` followed by ``paged_attention`` bit for bit."""
+    if queries.dim() != 4 or queries.shape[2] != 1:
+        raise ValueError("queries must be [B, H, 1, D]")
+    batch, heads, _, dim = queries.shape
+    shape = (batch, fmt.num_kv_heads, 1, dim)
+    if dim != fmt.head_dim or tuple(keys.shape) != shape or tuple(values.shape) != shape:
+        raise ValueError(f"keys and values must be {shape} and the queries' head dimension "
+                         "the page layout's")
+    for name, t in (("queries", queries), ("keys", keys), ("values", values)):
+        _check_float(t, fmt, name)
+    device = queries.device
+    table = _i32(block_table, device)
+    lens = _i32(seq_lens, device)
+    if waves <= 0:
+        waves = default_waves(fmt, heads, 1, batch)
+    need = workspace_bytes(fmt, heads, 1, waves)
+    if need < 0:
+        nat.check(nat.PKV_INVALID_ARGUMENT, "paged attention workspace")
+    if workspace is None:
+        workspace = attention_workspace(device, need)
+    elif workspace.device != device or workspace.dtype != torch.uint8 or \
+            not workspace.is_contiguous():
+        raise ValueError("attention workspace must be a contiguous uint8 tensor on the "
+                         "queries' device")
+    queries, keys, values = queries.contiguous(), keys.contiguous(), values.contiguous()
+    if out is None:
+        out = torch.empty(queries.shape, dtype=queries.dtype, device=device)
+    elif (tuple(out.shape) != tuple(queries.shape) or out.dtype != queries.dtype
+          or out.device != device or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous tensor of the queries' shape, dtype and "
+                         "device")
+    code = nat.load().pkv_append_paged_attention(
+        nat.stream_handle(device), fmt.c_layout, nat.ptr(pool), pool.shape[0], nat.ptr(keys),
+        nat.ptr(values), nat.ptr(queries), batch, heads, nat.ptr(table), table.shape[1],
+        nat.ptr(lens), float(scale), int(waves), nat.ptr(workspace), workspace.numel(),
+        nat.ptr(out))
+    nat.check(code, "append + paged attention")
+    return out
+
+
 def gather_pages(fmt: PageFormat, pool, page_ids):
     """Pages in the reference's per-page tensor format (``paged_attention.py:31-35``).
 

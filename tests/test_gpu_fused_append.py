@@ -1,0 +1,165 @@
+"""GPU: the fused single-token step (``pkv_append_paged_attention``) through the C ABI.
+
+One launch appends each sequence's new K/V token and attends its query where
+the decode kernel serves the shape (quantized pages, <= 8 query rows per KV
+head); other shapes run an append launch and the attention.  Either way the
+pages and the output must equal ``pkv_append_quantize`` followed by
+``pkv_paged_attention`` bit for bit (same kernels' arithmetic, same work
+split), and the output must meet the oracle's bar (``engine/paged.py:260-263``
+is the reference's append-then-attend pair).
+"""
+
+from __future__ import annotations
+
+import types
+
+import numpy as np
+import pytest
+
+from paged_case import assert_attention_close, fill_pages, oracle_attention, scale_of, to_torch
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pkv import _native
+
+    _native.load()
+
+
+def _fmt(w, dtype=None):
+    from pkv.ops import PageFormat
+
+    return PageFormat(w.kv_heads, w.head_dim, w.page_tokens, w.bits, w.group_size,
+                      dtype or torch.bfloat16)
+
+
+def _context_pool(fmt, inst):
+    """A pool holding every sequence's tokens but the last (the step's new
+    one); returns ``(pool, table, lengths after the step)``."""
+    from pkv import ops
+
+    lens = np.array([k.shape[1] for k in inst.keys])
+    table = torch.from_numpy(inst.table).cuda()
+    if (lens > 1).any():
+        ctx = types.SimpleNamespace(workload=inst.workload, table=inst.table,
+                                    num_pages=inst.num_pages,
+                                    keys=[k[:, :-1] for k in inst.keys],
+                                    values=[v[:, :-1] for v in inst.values])
+        pool, table, _ = fill_pages(fmt, ctx, chunk=64)
+    else:
+        pool = ops.allocate_pool(fmt, inst.num_pages)
+    return pool, table, torch.from_numpy(lens.astype(np.int32)).cuda()
+
+
+def _new_rows(inst, fmt):
+    k = np.stack([kk[:, -1:] for kk in inst.keys])     # [B, HK, 1, D]
+    v = np.stack([vv[:, -1:] for vv in inst.values])
+    return to_torch(k, fmt.dtype), to_torch(v, fmt.dtype)
+
+
+CASES = {
+    # name: (workload overrides, waves); every case is a single-token step
+    "c2_small_default_waves": (dict(name="c2", batch=6, length_range=(1, 700)), 0),
+    "c2_small_waves_3": (dict(name="c2", batch=5, length_range=(17, 900)), 3),
+    "c2_many_waves_short_pieces": (dict(name="c2", batch=4, lengths=(33, 1, 200, 64)), 500),
+    "c2_one_wave": (dict(name="c2", batch=3, lengths=(1500, 16, 31)), 1),
+    "every_tile_position": (dict(name="c2", batch=16, lengths=tuple(range(100, 116))), 0),
+    "gqa8_slots2_4bit_g32": (dict(name="c3", batch=3, lengths=(300, 47, 1030), group_size=32), 0),
+    "int8_d100_p32": (dict(name="c2", batch=4, lengths=(90, 7, 260, 33), head_dim=100,
+                           group_size=32, page_tokens=32), 9),
+    "int4_d64_p64": (dict(name="c2", batch=3, lengths=(129, 64, 5), bits=4, head_dim=64,
+                          group_size=32, page_tokens=64), 0),
+    "b80_chunks": (dict(name="c2", batch=80, length_range=(1, 300)), 37),
+    # served by two launches inside the entry point
+    # (no outlier channels: float pages take P as a bf16 MFMA operand, 2^-9
+    # relative, which stays inside the bar for values of N(0,1) size)
+    "fallback_bf16_pages": (dict(name="c2", batch=3, lengths=(40, 3, 70), bits=16,
+                                 group_size=32, outlier_fraction=0.0), 0),
+    "fallback_rows16": (dict(name="c2", batch=3, lengths=(50, 18, 200), heads=32, kv_heads=2), 0),
+}
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_fused_step_equals_append_then_attend(case):
+    from pkv import ops, workloads
+
+    overrides, waves = CASES[case]
+    overrides = dict(overrides)
+    w = workloads.get(overrides.pop("name"), num_queries=1, append_tokens=1,
+                      shared_prefix_pages=0, **overrides)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    k_new, v_new = _new_rows(inst, fmt)
+    q = to_torch(inst.queries, fmt.dtype)
+    scale = scale_of(w.head_dim)
+    # separate: append at L - 1, then attend
+    pool_a, table, lens = _context_pool(fmt, inst)
+    ops.append_quantize(fmt, pool_a, k_new, v_new, table, lens - 1)
+    want_out = ops.paged_attention(fmt, pool_a, q, table, lens, scale=scale, waves=waves)
+    # fused
+    pool_b, _, _ = _context_pool(fmt, inst)
+    got_out = ops.append_paged_attention(fmt, pool_b, k_new, v_new, q, table, lens, scale=scale,
+                                         waves=waves)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a, pool_b), "pages differ"
+    assert torch.equal(want_out, got_out), "outputs differ"
+    want = oracle_attention(fmt, inst, inst.positions, np.ones(w.batch, np.int32), scale)
+    assert_attention_close(got_out.float().cpu().numpy(), want)
+
+
+def test_fused_step_c2_full_size_against_the_oracle():
+    """C2 at its stated size: the context filled by appends, then one fused
+    step; pages (bit-exact, against the C oracle's quantizer) and attention as
+    in the full-size parity test."""
+    import math
+
+    from oracle import cport
+    from paged_case import assert_attention_close_f32
+    from pkv import ops, workloads
+    from test_gpu_fullsize import append, check_pages_bit_exact, oracle_arrays
+
+    w = workloads.get("c2")
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    context = inst.context.astype(np.int64)
+    total = inst.total_lengths.astype(np.int64)
+    pool = ops.allocate_pool(fmt, inst.num_pages)
+    append(fmt, pool, w, inst.keys, inst.values, inst.table, np.zeros_like(context), context)
+    k_new, v_new = _new_rows(inst, fmt)
+    lens = torch.from_numpy(total.astype(np.int32)).cuda()
+    table = torch.from_numpy(inst.table).cuda()
+    scale = 1.0 / math.sqrt(w.head_dim)
+    out = ops.append_paged_attention(fmt, pool, k_new, v_new, to_torch(inst.queries, fmt.dtype),
+                                     table, lens, scale=scale)
+    torch.cuda.synchronize()
+    arrays, counts = oracle_arrays(w, inst.keys, inst.values, inst.table, inst.num_pages)
+    pages = check_pages_bit_exact(fmt, pool, arrays, counts)
+    want = cport.paged_attention(inst.queries, inst.table, total, inst.positions, inst.widths,
+                                 heads_kv=w.kv_heads, page_tokens=w.page_tokens, bits=w.bits,
+                                 group_size=w.group_size, pages=arrays, scale=scale)
+    worst, mean, over = assert_attention_close_f32(out.float().cpu().numpy(), want)
+    print(f"fused c2: {pages} pages bit-exact; attention max abs {worst:.2e}, mean abs "
+          f"{mean:.2e}, {over} elements over 2e-2")
+    assert over == 0
+
+
+def test_fused_step_rejects_bad_shapes():
+    from pkv import ops, workloads
+
+    w = workloads.get("c2", batch=2, lengths=(10, 20), num_queries=1, append_tokens=1)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lens = _context_pool(fmt, inst)
+    k_new, v_new = _new_rows(inst, fmt)
+    q = to_torch(inst.queries, fmt.dtype)
+    with pytest.raises(ValueError):
+        ops.append_paged_attention(fmt, pool, k_new[:, :, :0], v_new, q, table, lens, scale=0.1)
+    with pytest.raises(ValueError):
+        ops.append_paged_attention(fmt, pool, k_new, v_new, q.repeat(1, 1, 2, 1), table, lens,
+                                   scale=0.1)
