@@ -258,6 +258,14 @@ class DeviceBatchCache:
         read (the reservation fixes the positions on the device)."""
         fmt, pool = self.arena.fmt, self.arena.pools[self.layer]
         dtype = fmt.dtype
+        if queries.shape[2] == 1:
+            # a decode step (every width 1): the new token at lens - 1, its
+            # query there too -- one fused append + attention call
+            out = ops.append_paged_attention(fmt, pool, keys.to(dtype), values.to(dtype),
+                                             queries.to(dtype), self.res.table, self.res.lens,
+                                             scale=scale, waves=self.waves,
+                                             workspace=self.workspace)
+            return out.to(queries.dtype)
         ops.append_quantize(fmt, pool, keys.to(dtype).contiguous(), values.to(dtype).contiguous(),
                             self.res.table, self.res.starts, self.res.widths)
         out = ops.paged_attention(fmt, pool, queries.to(dtype).contiguous(), self.res.table,
