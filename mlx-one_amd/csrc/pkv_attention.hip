@@ -310,6 +310,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   using FO = FloatOps<QUANT ? 1 : FK>;
   using KT = typename FO::KT;
   using VT = typename FO::VT;
+  // bf16 pages: P enters the PV MFMA as a bf16 pair hi + lo (16 significant
+  // bits).  One bf16 alone is 2^-9 relative, which values of outlier channels
+  // (|v| ~ 30) turn into more than the output tolerance on short sequences.
+  constexpr bool SPLITP = !QUANT && FK == 0;
 
   // Lane-derived values are refreshed at every piece through an opaque copy
   // of the lane id, so the compiler recomputes per-lane addresses inside the
@@ -913,6 +917,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         }
       }
       VT pop[RB][NG];
+      VT plo[SPLITP ? RB : 1];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         float p[4];
@@ -946,6 +951,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           }
         } else {
           pop[rb][0] = FO::pack_p(p[0], p[1], p[2], p[3]);
+          if constexpr (SPLITP) plo[rb] = FO::pack_lo(p[0], p[1], p[2], p[3], pop[rb][0]);
         }
       }
       if constexpr (!QUANT) {
@@ -967,14 +973,15 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
         if (cmask & (1 << j)) {
-          VT bop[RB][NG];
+          VT bop[RB][NG], blo[SPLITP ? RB : 1];
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
+          for (int rb = 0; rb < RB; ++rb) {
+            const u2 zero = {0, 0};
 #pragma unroll
-            for (int gi = 0; gi < NG; ++gi) {
-              const u2 zero = {0, 0};
+            for (int gi = 0; gi < NG; ++gi)
               bop[rb][gi] = (SLOTS == 1 || slot_l == j) ? pop[rb][gi] : __builtin_bit_cast(VT, zero);
-            }
+            if constexpr (SPLITP) blo[rb] = (SLOTS == 1 || slot_l == j) ? plo[rb] : __builtin_bit_cast(VT, zero);
+          }
 #pragma unroll
           for (int n = 0; n < NB; ++n) {
             VT vop;
@@ -986,7 +993,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             }
             const int gi = QUANT ? (16 * n) / G : 0;
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) O[rb][n] = FO::pv(vop, bop[rb][gi], O[rb][n]);
+            for (int rb = 0; rb < RB; ++rb) {
+              O[rb][n] = FO::pv(vop, bop[rb][gi], O[rb][n]);
+              if constexpr (SPLITP) O[rb][n] = FO::pv(vop, blo[rb], O[rb][n]);
+            }
           }
         }
       }

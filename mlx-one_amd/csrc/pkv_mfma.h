@@ -144,6 +144,12 @@ struct FloatOps<0> {  // bf16 pages
     return s4{(short)f32_to_bf16_bits(p0), (short)f32_to_bf16_bits(p1),
               (short)f32_to_bf16_bits(p2), (short)f32_to_bf16_bits(p3)};
   }
+  // The rounding error of pack_p, itself rounded to bf16: P = hi + lo carries
+  // 16 significant bits (p - hi is exact in f32).
+  static __device__ __forceinline__ s4 pack_lo(float p0, float p1, float p2, float p3, s4 hi) {
+    auto up = [](short h) { return __uint_as_float((uint32_t)(uint16_t)h << 16); };
+    return pack_p(p0 - up(hi[0]), p1 - up(hi[1]), p2 - up(hi[2]), p3 - up(hi[3]));
+  }
 };
 
 

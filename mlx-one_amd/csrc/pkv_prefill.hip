@@ -110,11 +110,12 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];
   OT qv[RB][KB];
-  // f16 operands hold at most 65504: a row whose largest pre-scaled element
-  // reaches 2^15 is scaled by a power of two sc into [2^14, 2^15) (exact);
-  // its scores then leave the MFMA multiplied by sc, undone by isc
-  float sc[RB], isc[RB];
-  bool qscaled = false;
+  // The query operand is the query itself (bf16 -> f16 is exact in range);
+  // scale*log2(e) is applied to the f32 scores (rsc), never rounded into the
+  // operand.  f16 operands hold at most 65504: a row whose largest element
+  // reaches 2^15 is scaled by a power of two sc into [2^14, 2^15) (exact),
+  // which its rsc undoes.
+  float sc[RB], rsc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
@@ -141,29 +142,26 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (!valid || d0 + e >= g.dim) e8[e] = 0;
-      // queries pre-scaled by scale*log2(e): scores leave the MFMA in the
-      // exp2 domain
       OT v;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = bits_to_float(e8[e], g.float_kind) * a.scale_log2;
+        const float x = bits_to_float(e8[e], g.float_kind);
         mx = fmaxf(mx, fabsf(x));
         if constexpr (F16) v[e] = (_Float16)x;
         else v[e] = (__bf16)x;
       }
       qv[rb][kb] = v;
     }
-    sc[rb] = isc[rb] = 1.0f;
+    sc[rb] = 1.0f;
     if constexpr (F16) {
-      // the row's largest |q * scale * log2(e)| (lanes jj share the row);
-      // a scaled row converts again from memory (rare: huge queries only)
+      // the row's largest |q| (lanes jj share the row); a scaled row
+      // converts again from memory (rare: huge queries only)
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       if (mx >= 32768.0f && mx < INFINITY) {
         int ex;
         frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
         sc[rb] = ldexpf(1.0f, 15 - ex);
-        isc[rb] = ldexpf(1.0f, ex - 15);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const int d0 = 32 * kb + 8 * jj;
@@ -171,15 +169,14 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const uint16_t bits = valid && d0 + e < g.dim ? qrow[d0 + e] : 0;
-            v[e] = (_Float16)(bits_to_float(bits, g.float_kind) * a.scale_log2 * sc[rb]);
+            v[e] = (_Float16)(bits_to_float(bits, g.float_kind) * sc[rb]);
           }
           qv[rb][kb] = v;
         }
       }
     }
-    qscaled |= sc[rb] != 1.0f;
+    rsc[rb] = a.scale_log2 / sc[rb];  // sc is a power of two: exact
   }
-  qscaled = __any(qscaled);
 
   // ---- the block's visible span: tokens up to the largest limit; tiles
   // below the smallest live limit are seen whole by every live row
@@ -364,16 +361,15 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     return __builtin_elementwise_maximum(b3, c3);
   };
 
-  // ---- one step covers tiles 4s + 2pr and 4s + 2pr + 1 of a stage image.
-  // S^T = K.Q^T for both tiles.  The accumulators start at -mb (the running
-  // max, 0 before any token is seen), so the MFMAs leave v = s - mb.
+  // ---- one step covers tiles 2pr and 2pr + 1 of a stage image.
+  // S^T = K.Q^T for both tiles; the scores then become v = s*rsc - mb in the
+  // exp2 domain (mb: the running max, 0 before any token is seen).
   auto qk = [&](const uint16_t *img, int pr, f4 (&S)[2][RB], float (&mb)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       mb[rb] = m[rb] == -INFINITY ? 0.0f : m[rb];
-      const float init = -mb[rb] * sc[rb];  // scaled rows: the MFMA sums carry sc
 #pragma unroll
-      for (int i = 0; i < 2; ++i) S[i][rb] = f4{init, init, init, init};
+      for (int i = 0; i < 2; ++i) S[i][rb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     const uint16_t *kbase = img + 2 * pr * I::KTILE + col * I::KROW + 8 * jj;
 #pragma unroll
@@ -406,11 +402,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = S[i][rb][r];
-      if (qscaled) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[rb][e] *= isc[rb];
-      }
+        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = __builtin_fmaf(S[i][rb][r], rsc[rb], -mb[rb]);
       if (!fast) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -445,8 +437,11 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       }
     }
   };
-  // P = exp2(v) (masked: exp2(-inf) = 0), row sums, packed operand
-  auto probs = [&](const float (&v)[RB][8], OT (&P)[RB]) __attribute__((always_inline)) {
+  // P = exp2(v) (masked: exp2(-inf) = 0), row sums, packed operand; bf16
+  // pages also pack the rounding error Plo (P = hi + lo: 16 significant bits,
+  // where one bf16 alone, 2^-9 relative, times values of outlier channels
+  // exceeds the output tolerance on short spans)
+  auto probs = [&](const float (&v)[RB][8], OT (&P)[RB], OT (&Plo)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float p[8];
@@ -459,11 +454,15 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       } else {
         P[rb] = b8{(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3],
                    (__bf16)p[4], (__bf16)p[5], (__bf16)p[6], (__bf16)p[7]};
+        OT lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(p[e] - (float)P[rb][e]);
+        Plo[rb] = lo;
       }
     }
   };
   // O^T += V^T.P^T over the step's 32 tokens
-  auto pv = [&](const uint16_t *img, int pr, const OT (&P)[RB]) __attribute__((always_inline)) {
+  auto pv = [&](const uint16_t *img, int pr, const OT (&P)[RB], const OT (&Plo)[RB]) __attribute__((always_inline)) {
     const uint16_t *vbase = img + I::K_ELEMS + col * I::VROW + 32 * pr + 8 * jj;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
@@ -472,8 +471,10 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       for (int rb = 0; rb < RB; ++rb) {
         if constexpr (F16)
           O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, P[rb], O[rb][n], 0, 0, 0);
-        else
+        else {
           O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, P[rb], O[rb][n], 0, 0, 0);
+          O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, Plo[rb], O[rb][n], 0, 0, 0);
+        }
       }
     }
   };
@@ -515,14 +516,14 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     constexpr int NPAIR = kStageTiles / 2;
     f4 S[2][2][RB];
     float mb[2][RB], v[RB][8];
-    OT P[RB];
+    OT P[RB], Plo[RB];
     qk(img, 0, S[0], mb[0]);
 #pragma unroll
     for (int pr = 0; pr < NPAIR; ++pr) {
       scores(S[pr & 1], mb[pr & 1], s, pr, okv, v);
       if (pr + 1 < NPAIR) qk(img, pr + 1, S[(pr + 1) & 1], mb[(pr + 1) & 1]);
-      probs(v, P);
-      pv(img, pr, P);
+      probs(v, P, Plo);
+      pv(img, pr, P, Plo);
       if (pr == 0) {
         convert(buf ^ 1, true);
         if (s + 2 < nstages) fetch_k(s + 2);

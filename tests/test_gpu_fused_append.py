@@ -77,10 +77,8 @@ CASES = {
                           group_size=32, page_tokens=64), 0),
     "b80_chunks": (dict(name="c2", batch=80, length_range=(1, 300)), 37),
     # served by two launches inside the entry point
-    # (no outlier channels: float pages take P as a bf16 MFMA operand, 2^-9
-    # relative, which stays inside the bar for values of N(0,1) size)
     "fallback_bf16_pages": (dict(name="c2", batch=3, lengths=(40, 3, 70), bits=16,
-                                 group_size=32, outlier_fraction=0.0), 0),
+                                 group_size=32), 0),
     "fallback_rows16": (dict(name="c2", batch=3, lengths=(50, 18, 200), heads=32, kv_heads=2), 0),
 }
 

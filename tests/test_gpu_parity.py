@@ -409,15 +409,15 @@ QUERY_SCALE_CASES = {
 }
 
 
-# The chunked-prefill kernel dequantizes K to f16 and pre-scales queries by
-# scale*log2(e) into f16 (one rounding each, relative 2^-11), which is what
-# keeps it MFMA-bound; its score error grows with |q|*|k| and passes the
-# 2e-2 bar up to about 10x N(0,1) queries (a CPU emulation of the two
-# roundings gives 1.3e-2 at 10x, 3.4e-2 at 30x, 0.24 at 300x).  The decode and
-# verify kernels keep codes exact and apply scales in f32, at any magnitude.
+# The chunked-prefill kernel dequantizes K to f16 once per stage (one
+# rounding, relative 2^-11), which is what keeps it MFMA-bound; the query
+# operand is exact and scale*log2(e) is applied to the f32 scores.  Its score
+# error still grows with |q|*|k|: the 10x queries pass the 2e-2 bar, 30x and
+# beyond do not.  The decode and verify kernels keep codes exact and apply
+# scales in f32, at any magnitude.
 _PREFILL_LIMIT = pytest.mark.xfail(
-    strict=True, reason="prefill kernel: K and pre-scaled queries in f16, error grows with "
-                        "|q|*|k| (within the bar up to ~10x N(0,1) queries)")
+    strict=True, reason="prefill kernel: K dequantized to f16, error grows with |q|*|k| "
+                        "(within the bar up to ~10x N(0,1) queries)")
 
 
 def _scale_params():
