@@ -45,15 +45,18 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 constexpr int prefill_rb(int dp) { return dp > 128 ? 1 : 2; }
 constexpr int prefill_rows(int dp) { return prefill_waves(dp) * 16 * prefill_rb(dp); }
 
-// LDS image of one stage (u16 elements).  Rows padded by 8 elements so that
-// the 16 lanes of a ds_read_b128 phase hit distinct banks (row strides of
-// 2*(DP+8) and 272 bytes).
+// LDS image of one stage (u16 elements).  The operand reads are ds_read_b128
+// with lane (col, jj) at byte col*stride + 16*jj.  On gfx950 such a read runs
+// without bank conflicts when the row stride is 16*k bytes with k = 2 (mod 4)
+// (measured: 288, 352, 416, 480, 544 conflict-free; 272 and 304 two-way, 256
+// eight-way), so rows are padded by 16 elements: strides of 2*(DP+16) bytes
+// (160, 288, 544) and 2*(16*TILES+16) bytes (288 at 8 tiles, 160 at 4).
 template <int DP>
 struct StageImage {
   static constexpr int TILES = prefill_waves(DP);
-  static constexpr int KROW = DP + 8;           // K row: one token
+  static constexpr int KROW = DP + 16;          // K row: one token
   static constexpr int KTILE = 16 * KROW;
-  static constexpr int VROW = 16 * TILES + 8;   // V^T row: one dim, 16 token slots per tile
+  static constexpr int VROW = 16 * TILES + 16;  // V^T row: one dim, 16 token slots per tile
   static constexpr int K_ELEMS = TILES * KTILE;
   static constexpr int ELEMS = K_ELEMS + DP * VROW;
 };
