@@ -219,41 +219,40 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   uint32_t rk[LW], rv[LW];
   uint32_t rkm[QUANT ? NG : 1], rvm[QUANT ? 4 * NG : 4];
   int k_ok = 0, k_t = 0, v_ok = 0, v_t = 0;  // tile whose K (V) half sits in rk (rv)
-  // Page ids of the sequence, 64 per window: lane i holds entry wbase + i;
-  // the next window is loaded 64 pages ahead, so a lookup is one readlane.
-  const int32_t *trow = a.table + (int64_t)b * a.max_pages;
-  auto load_ids = [&](int base) __attribute__((always_inline)) {
-    const int p = base + lane;
-    return p < a.max_pages ? trow[p] : -1;
-  };
-  int wbase = 0;
-  int pwin = load_ids(0), pnext = load_ids(64);
-  // tile 4s + wv of stage s -> (present, tile, head block, tile offset)
-  auto locate = [&](int s, int &ok, int &t, const uint8_t *&head, int &tip) __attribute__((always_inline)) {
-    t = s * kStageTiles + wv;
+  // Page id of a tile: one uniform (scalar) load of the block table per
+  // stage; the K and V halves of a tile share it.  (A page-id window held in
+  // a VGPR and read with v_readlane made every lookup wait for all vector
+  // loads in flight, the tile loads just issued included.)
+  typedef __attribute__((address_space(4))) const int32_t cint32;  // read-only: scalar loads
+  cint32 *trow = (cint32 *)(a.table + (int64_t)b * a.max_pages);
+  int n_ok = 0, n_t = 0, n_tip = 0;  // the located tile
+  const uint8_t *n_head = a.pool;
+  // tile kStageTiles*s + wv of stage s -> (present, tile, head block, tile offset)
+  auto locate = [&](int s) __attribute__((always_inline)) {
+    n_t = s * kStageTiles + wv;
     int id = -1;
-    tip = 0;
-    if (t < ntiles) {
-      const int p = t >> tpp_shift;
-      if (p >= wbase + 64) {  // pages advance at most 8 per stage
-        pwin = pnext;
-        wbase += 64;
-        pnext = load_ids(wbase + 64);
-      }
-      const int pid = __builtin_amdgcn_readlane(pwin, p - wbase);
+    n_tip = 0;
+    if (n_t < ntiles) {
+      const int p = n_t >> tpp_shift;
+      const int pid = p < a.max_pages ? trow[p] : -1;
       if (pid >= 0 && pid < a.num_pages) {
         id = pid;
-        tip = t & tpp_mask;
+        n_tip = n_t & tpp_mask;
       }
     }
-    ok = id >= 0;
-    head = a.pool + (int64_t)(ok ? id : 0) * g.page_bytes + (int64_t)kh * g.head_bytes;
+    n_ok = id >= 0;
+    n_head = a.pool + (int64_t)(n_ok ? id : 0) * g.page_bytes + (int64_t)kh * g.head_bytes;
   };
-  auto fetch_k = [&](int s) __attribute__((always_inline)) {
-    const uint8_t *head;
-    int tip;
-    locate(s, k_ok, k_t, head, tip);
-    if (k_ok) {
+  // Both halves of the wave's tile of stage s, issued together (so that the
+  // compiler's wait counts before the conversions are exact: a path with
+  // only one half issued would make it wait for every load in flight).
+  auto fetch = [&](int s) __attribute__((always_inline)) {
+    locate(s);
+    k_ok = v_ok = n_ok;
+    k_t = v_t = n_t;
+    if (n_ok) {
+      const uint8_t *head = n_head;
+      const int tip = n_tip;
       load_payload<C>(rk, head + (int64_t)tip * g.tile_bytes, lane);
       if constexpr (QUANT) {
         const uint8_t *km = head + g.kmeta_offset + (int64_t)((tip * PKV_TILE + col) * NG) * 4;
@@ -270,13 +269,6 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
           }
         }
       }
-    }
-  };
-  auto fetch_v = [&](int s) __attribute__((always_inline)) {
-    const uint8_t *head;
-    int tip;
-    locate(s, v_ok, v_t, head, tip);
-    if (v_ok) {
       load_payload<C>(rv, head + g.v_offset + (int64_t)tip * g.tile_bytes, lane);
       if constexpr (QUANT)
         load_meta<C>(rvm, head + g.vmeta_offset + (int64_t)((tip * PKV_TILE + 4 * jj) * NG) * 4);
@@ -484,22 +476,18 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 
   // ---- stream the span.  Iteration s computes stage s from image s&1,
   // converts the tile of stage s+1 (loaded during stage s-1) into image
-  // (s+1)&1 -- last read in iteration s-1, before its barrier -- and issues
-  // the loads of stage s+2.  Within a stage the second step's QK MFMAs are
+  // (s+1)&1 -- last read in iteration s-1, before its barrier -- and, after
+  // its V half, issues the loads of stage s+2.  Within a stage the second step's QK MFMAs are
   // issued before the first step's exponentials and the conversion halves
   // sit beside the PV MFMAs, so that the MFMA and VALU pipes overlap.  Both
   // run without branches: past the span the second step sees tiles flagged
   // invalid (zeros, fully masked), and the last stage converts its own tile
   // once more into the image nobody reads again.
   if (nstages > 0) {
-    fetch_k(0);
-    fetch_v(0);
+    fetch(0);
     convert(0, true);
     convert(0, false);
-    if (nstages > 1) {
-      fetch_k(1);
-      fetch_v(1);
-    }
+    if (nstages > 1) fetch(1);
   }
   lds_barrier();
   for (int s = 0; s < nstages; ++s) {
@@ -529,10 +517,9 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       pv(img, pr, P, Plo);
       if (pr == 0) {
         convert(buf ^ 1, true);
-        if (s + 2 < nstages) fetch_k(s + 2);
       } else if (pr == 1) {
         convert(buf ^ 1, false);
-        if (s + 2 < nstages) fetch_v(s + 2);
+        if (s + 2 < nstages) fetch(s + 2);
       }
     }
     lds_barrier();
