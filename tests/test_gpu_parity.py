@@ -167,6 +167,8 @@ ATTN_CASES = {
     "c2_g32_f16": (dict(name="c2", batch=3, length_range=(100, 400), group_size=32), "float16",
                    64, 3),
     "c2_one_wave_long": (dict(name="c2", batch=2, lengths=(2100, 1500)), "bfloat16", 256, 1),
+    # one piece of 313 pages: the 64-page window slides four times
+    "c2_one_wave_two_slides": (dict(name="c2", batch=1, lengths=(5000,)), "bfloat16", 512, 1),
     "c3_small": (dict(name="c3", batch=2, lengths=(1500, 2048)), "bfloat16", 512, 0),
     "c3_partitions512": (dict(name="c3", batch=2, lengths=(2048, 2048)), "bfloat16", 512, 32),
     "c3_one_wave_long": (dict(name="c3", batch=1, lengths=(4100,)), "bfloat16", 512, 1),
