@@ -69,13 +69,13 @@ constexpr int fit_slots(int bits, int dp, int g, int slots) {
 // Shapes whose register needs sit just above 256 VGPRs: asking for two waves
 // per SIMD costs them at most a few spills outside the tile loop and doubles
 // their occupancy.  Others keep the compiler's choice (heavier shapes would
-// spill inside the loop).
+// spill inside the loop: int8 D256 G128 forced to two waves spilled 98 VGPRs
+// and ran 5.6% slower than at one wave per SIMD).
 constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
   return (bits == 8 && dp == 128 && g == 64 && rb == 1 && slots == 4) ||
                  (bits == 4 && dp == 128 && g == 32 && rb == 1 && slots == 4) ||
                  (bits == 4 && dp == 128 && g == 64 && rb == 2) ||
-                 (bits == 8 && dp == 128 && g == 64 && rb == 2) ||
-                 (bits == 8 && dp == 256 && g == 128 && rb == 1)
+                 (bits == 8 && dp == 128 && g == 64 && rb == 2)
              ? 2
              : 1;
 }
