@@ -343,7 +343,7 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     a.narrow_lo = t.lo;
     a.narrow_q = t.hi;
     a.waves = t.waves;
-    a.lead = pkv::attention_lead(a.g, a.rows);
+    a.lead = pkv::attention_lead(a.g, a.rows, fused != nullptr);
     a.part_ml = (float *)((char *)workspace + t.ws.ml);
     a.part_acc = (float *)((char *)workspace + t.ws.acc);
     if (fused) {

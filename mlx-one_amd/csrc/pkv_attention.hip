@@ -86,12 +86,6 @@ __device__ __forceinline__ int seq_tiles(int len) {
   return len <= 0 ? 1 : (len + PKV_TILE - 1) / PKV_TILE;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 // Work split.  Split tiles are numbered over (sequence b, KV head kh) in that
 // order, T in all: each (b, kh) segment spans `lead` tiles with no data, then
 // its own tiles.  Wave w of W (W <= T) owns the run [start(w), start(w+1)):
@@ -245,13 +239,30 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
       }
     }
   }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sm, o, 64);
+  // combine across lanes: within 16-lane rows by DPP exchanges (the
+  // combination is symmetric, so both lanes of a pair hold the same bits),
+  // then the four rows' results, read as uniform values, in row order
+  auto combine = [&](float om, float os) __attribute__((always_inline)) {
     const float nm = fmaxf(mx, om);
     sm = nm == -INFINITY ? 0.0f
                          : sm * __builtin_amdgcn_exp2f(mx - nm) + os * __builtin_amdgcn_exp2f(om - nm);
     mx = nm;
+  };
+  combine(row_xchg<0xB1>(mx), row_xchg<0xB1>(sm));
+  combine(row_xchg<0x4E>(mx), row_xchg<0x4E>(sm));
+  combine(row_xchg<0x141>(mx), row_xchg<0x141>(sm));
+  combine(row_xchg<0x140>(mx), row_xchg<0x140>(sm));
+  {
+    float rm[4], rs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      rm[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16 * r));
+      rs[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sm), 16 * r));
+    }
+    mx = rm[0];
+    sm = rs[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) combine(rm[r], rs[r]);
   }
   const float inv = 1.0f / fmaxf(sm, 1e-20f);
   // lane l: weight 2^(m - M) / S of piece l
@@ -504,8 +515,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       if constexpr (QUANT) {
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-          qs[rb][gi] += __shfl_xor(qs[rb][gi], 16, 64);
-          qs[rb][gi] += __shfl_xor(qs[rb][gi], 32, 64);
+          qs[rb][gi] = xor32_add(xor16_add(qs[rb][gi]));
         }
       }
     }
@@ -554,15 +564,18 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   auto tile_at = [&](int pkh, int id, int t) __attribute__((always_inline)) {
     return a.pool + (int64_t)id * g.page_bytes + (int64_t)pkh * g.head_bytes + (int64_t)t * g.tile_bytes;
   };
-  // the lane's metadata words (its slot's tile of iteration `it`, tokens 4*jj..4*jj+3)
-  auto meta_at = [&](int pkh, int pta, int ntl, int pwin, int ppid, int it, int64_t side)
+  // the lane's metadata words: its slot's tile of an iteration as plan()
+  // placed it (absent tiles: page 0, tile 0), tokens 4*jj..4*jj+3; the page
+  // id comes from plan's uniform values by selects (no lane permute)
+  auto meta_at = [&](int pkh, const int (&pg)[SLOTS], const int (&tp)[SLOTS], int64_t side)
       __attribute__((always_inline)) {
-    const int tile = it * SLOTS + slot_l;
-    const int st = pta + tile;
-    const int id = __shfl(ppid, ((st >> tpp_shift) - pwin) & 63, 64);
-    const bool ok = tile < ntl && id >= 0;
-    const int64_t h = (int64_t)pkh * g.head_bytes + (ok ? (int64_t)id * g.page_bytes : 0);
-    const int t = ok ? st & tpp_mask : 0;
+    int id = pg[0], t = tp[0];
+#pragma unroll
+    for (int j = 1; j < SLOTS; ++j) {
+      id = slot_l == j ? pg[j] : id;
+      t = slot_l == j ? tp[j] : t;
+    }
+    const int64_t h = (int64_t)pkh * g.head_bytes + (int64_t)id * g.page_bytes;
     return a.pool + h + side + (int64_t)(t * PKV_TILE + 4 * jj) * (NG * 4);
   };
 
@@ -741,8 +754,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       }
       fetch_q(cb, ckh, raw, qp);
       cmask = plan(cta, ntl, cwin, cpid, 0, pg, tp);
-      load_k(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.kmeta_offset));
-      load_v(ckh, pg, tp, meta_at(ckh, cta, ntl, cwin, cpid, 0, g.vmeta_offset));
+      load_k(ckh, pg, tp, meta_at(ckh, pg, tp, g.kmeta_offset));
+      load_v(ckh, pg, tp, meta_at(ckh, pg, tp, g.vmeta_offset));
       set_queries(cL, width, t1, raw, qp);
       // the new token: quantized and stored while the piece's first tiles
       // are in flight (it is patched into the registers of the piece's last
@@ -870,18 +883,28 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           cpid = fetch_window(cb, cwin, t1);
         }
         nmask = plan(cta, ntl, cwin, cpid, it + 1, npg, ntp);
-        load_k(ckh, npg, ntp, meta_at(ckh, cta, ntl, cwin, cpid, it + 1, g.kmeta_offset));
-        nmv = meta_at(ckh, cta, ntl, cwin, cpid, it + 1, g.vmeta_offset);
+        load_k(ckh, npg, ntp, meta_at(ckh, npg, ntp, g.kmeta_offset));
+        nmv = meta_at(ckh, npg, ntp, g.vmeta_offset);
         __builtin_amdgcn_sched_barrier(0);
       }
       if (__any(need)) {
-        // move a column's running max (column = same lane across jj)
+        // Until a column sees its first visible token its running max is
+        // -inf and its sums and O^T are exact zeros: while that holds for
+        // every column (a piece's first iteration), the max moves without
+        // the rescale.
+        bool fresh = true;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) fresh &= m[rb] == -INFINITY;
+        const bool rescale = !__all(fresh);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           float tm = fmaxf(fmaxf(s[rb][0], s[rb][1]), fmaxf(s[rb][2], s[rb][3]));
-          tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-          tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+          tm = xor32_max(xor16_max(tm));
           const float mn = fmaxf(m[rb], tm);
+          if (!rescale) {
+            m[rb] = mn;
+            continue;
+          }
           const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[rb] - mn);
           m[rb] = mn;
           lsum[rb] *= alpha;
@@ -1019,18 +1042,15 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     const int slot = cfirst ? 2 * w : 2 * w + 1;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
-      lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
+      lsum[rb] = xor32_add(xor16_add(lsum[rb]));
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi) {
         if constexpr (MSUM) {  // already summed over the tokens of every lane
           corr[rb][gi] = csum[rb][gi][0];
           osum[rb][gi] = osum4[rb][gi][0];
         } else {
-          corr[rb][gi] += __shfl_xor(corr[rb][gi], 16, 64);
-          corr[rb][gi] += __shfl_xor(corr[rb][gi], 32, 64);
-          osum[rb][gi] += __shfl_xor(osum[rb][gi], 16, 64);
-          osum[rb][gi] += __shfl_xor(osum[rb][gi], 32, 64);
+          corr[rb][gi] = xor32_add(xor16_add(corr[rb][gi]));
+          osum[rb][gi] = xor32_add(xor16_add(osum[rb][gi]));
         }
       }
       float mrow = m[rb], lrow = lsum[rb], wgt = 1.0f;
@@ -1729,8 +1749,11 @@ int attention_waves(const Geo &g, int rows) {
 // a wave whose run crosses into another segment gets correspondingly fewer
 // tiles and ends with the others.  Eight tiles measured best, or within
 // noise of it, for 1, 5 and 20 rows per KV head and contexts from 64 to
-// 16K tokens (4-slot decode: about two iterations).
-int attention_lead(const Geo &, int) { return 8; }
+// 16K tokens (4-slot decode: about two iterations).  A launch that fuses the
+// single-token append charges 16: the wave that holds a segment's last tile
+// (the one whose run crosses into the next segment) also loads and quantizes
+// the new token before its first tiles (C2: 67.8 us against 69.0 at 8).
+int attention_lead(const Geo &, int, bool append) { return append ? 16 : 8; }
 
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
   const AttnKernel k = select_kernel(a.g, a.rows, a.new_k != nullptr);

@@ -73,14 +73,53 @@ __device__ __forceinline__ int v4_byte(int r) {
   return r == 0 ? 0 : r == 1 ? 2 : r == 2 ? 1 : 3;
 }
 
-// Wave-wide inclusive prefix sum.
-__device__ __forceinline__ int wave_scan_incl(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
+// Wave-wide inclusive prefix sum on DPP moves (no LDS round trips): prefix
+// sums within each 16-lane row by row_shr 1, 2, 4, 8 (lanes shifted in from
+// before the row read 0), then row 1 and row 3 add lane 15 / 47
+// (row_bcast:15), rows 2 and 3 add lane 31 (row_bcast:31).  `lane` is unused.
+__device__ __forceinline__ int wave_scan_incl(int v, int /*lane*/) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
+}
+
+// Wave-wide sum, uniform (read from the scan's last lane).
+__device__ __forceinline__ int wave_sum(int v) {
+  return __builtin_amdgcn_readlane(wave_scan_incl(v, 0), 63);
+}
+
+// v + v[lane ^ 16] and v + v[lane ^ 32] (and the max forms) on the gfx950
+// permlane swaps, VALU only.  permlane16_swap(v, v) returns (row 0, row 0,
+// row 2, row 2 | row 1, row 1, row 3, row 3) as its two halves, and
+// permlane32_swap(v, v) (lanes < 32, lanes < 32 | lanes >= 32, lanes >= 32),
+// so each lane adds its own value and its partner's.
+__device__ __forceinline__ float xor16_add(float v) {
+  const auto z = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(z[0]) + __uint_as_float(z[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+  const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(z[0]) + __uint_as_float(z[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto z = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(z[0]), __uint_as_float(z[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(z[0]), __uint_as_float(z[1]));
+}
+
+// Lane exchange within 16-lane rows by a DPP pattern (every lane valid):
+// 0xB1 quad_perm xor 1, 0x4E quad_perm xor 2, 0x141 row_half_mirror
+// (lane i <-> 7 - i in each 8), 0x140 row_mirror (i <-> 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float row_xchg(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
 // Number of partitions of a sequence of `len` tokens (at least one, so that

@@ -137,8 +137,9 @@ hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a);
 // Resident waves of the attention kernel for this layout and row count on the
 // current device (CUs x workgroups per CU); <0 on error.
 int attention_waves(const Geo &g, int rows);
-// Lead tiles the decode split charges per segment for `rows` query rows per KV head.
-int attention_lead(const Geo &g, int rows);
+// Lead tiles the decode split charges per segment for `rows` query rows per KV
+// head (more for a launch that fuses the single-token append).
+int attention_lead(const Geo &g, int rows, bool append);
 // Whether the split-K decode kernel serves this many rows per KV head (else
 // launch_prefill does, with no workspace and no merge).
 bool decode_serves(const Geo &g, int rows);
