@@ -15,8 +15,11 @@ from the host instead); ``roofline.achieved`` divides the algorithmic bytes
 replay of the timed steps' attention launches, over the launch count
 (``roofline.kernel_timing``; beside it: the launch inside the step, step
 graph time minus an append-only graph's, and events around each launch of a
-host-launched pass, which add their own overhead).  Prints one JSON line
-(rank 0).
+host-launched pass, which add their own overhead).  For the HBM-bound
+decode workloads ``roofline.read_probe`` times ``pkv_read_probe`` -- a kernel
+that only reads every byte of the pages the step's sequences hold, at the
+same wave count -- the same way, and ``roofline.frac_of_read_probe`` compares
+the launch with it.  Prints one JSON line (rank 0).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--workload c2]
 """
@@ -455,6 +458,47 @@ def layer_device_bench(args):
     return 0
 
 
+def read_probe(lib, fmt, layers, table, lengths, waves, steps, device):
+    """Time ``pkv_read_probe`` over the pages the step's sequences hold (every
+    KV head, block-table order) at the decode launch's wave count, rotating
+    over the layer pools like the timed steps: one captured graph of ``steps``
+    launches between two HIP events.  Returns ``(ms per launch, bytes per
+    launch, pages)``."""
+    import numpy as np
+    import torch
+
+    from pkv import _native
+
+    pages = [table[b, :-(-int(n) // fmt.page_tokens)] for b, n in enumerate(lengths)]
+    ids = torch.from_numpy(np.concatenate(pages).astype(np.int32)).to(device)
+    out = torch.empty(waves * 64, dtype=torch.int32, device=device)
+    layout = fmt.c_layout
+
+    def launch(i):
+        pool = layers[i % len(layers)].pool
+        code = lib.pkv_read_probe(_native.stream_handle(device), layout, pool.data_ptr(),
+                                  pool.shape[0], ids.data_ptr(), ids.numel(), waves,
+                                  out.data_ptr())
+        if code:
+            _native.check(code, "read probe")
+
+    for i in range(len(layers)):
+        launch(i)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    span[0].record(torch.cuda.current_stream(device))
+    graph.replay()
+    span[1].record(torch.cuda.current_stream(device))
+    torch.cuda.synchronize()
+    ms = span[0].elapsed_time(span[1]) / steps
+    return ms, int(ids.numel()) * fmt.page_bytes, int(ids.numel())
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -708,6 +752,19 @@ def main(argv=None):
                                    else "attn_kernel")),
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
+    if roofline is not None and roofline["bound"] == "hbm" and graph is not None:
+        # the same pages read by a kernel that does nothing else
+        probe_ms, probe_bytes, probe_pages = read_probe(
+            lib, fmt, layers, inst.table, plans[args.warmup][3], waves, args.steps, device)
+        probe_gbs = probe_bytes / (probe_ms / 1e3) / 1e9
+        roofline["read_probe"] = {
+            "kernel_ms": round(probe_ms, 5), "achieved": round(probe_gbs, 1), "unit": "GB/s",
+            "frac": round(probe_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": probe_bytes,
+            "pages": probe_pages, "waves": waves,
+            "what": "pkv_read_probe: every byte of the pages the step's sequences hold "
+                    "(all KV heads), block-table order, equal runs over the attention's "
+                    "wave count, loads only; graph replay between HIP events"}
+        roofline["frac_of_read_probe"] = round(roofline["achieved"] / probe_gbs, 4)
     if roofline is not None:
         roofline["kernel_ms_events_per_launch"] = round(per_launch_ms, 5)
         if append_ms is not None:

@@ -191,6 +191,19 @@ int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const vo
 #define PKV_DECODE_VALU 1
 int pkv_select_decode_kernel(int kind);
 
+/*
+ * Measurement aid, no counterpart in the reference: a plain streaming read of
+ * whole pages (every KV head), page_ids[0..count) in order, split into equal
+ * runs over `waves` one-wave workgroups, each lane folding its loads into one
+ * word of out [waves * 64] uint32.  Given the pages a decode step's sequences
+ * hold, in block-table order, and the decode launch's wave count, its duration
+ * is what HBM takes to deliver those bytes to a kernel that does nothing else:
+ * the practical ceiling the decode launch is compared against.  Ids outside
+ * [0, num_pages) are skipped.
+ */
+int pkv_read_probe(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
+                   const int32_t *page_ids, int64_t count, int32_t waves, void *out);
+
 /* Waves the attention kernel keeps resident on the current device for this
  * layout and (num_heads, num_queries) (1 for query blocks served by the
  * prefill kernel).  <0 on error. */

@@ -503,6 +503,20 @@ int pkv_copy_pages(void *stream, const pkv_layout *layout, void *pool, int64_t n
                       "copy launch");
 }
 
+int pkv_read_probe(void *stream, const pkv_layout *layout, const void *pool, int64_t num_pages,
+                   const int32_t *page_ids, int64_t count, int32_t waves, void *out) {
+  pkv_geometry geo;
+  if (int rc = geometry(layout, &geo)) return rc;
+  if (count < 0 || num_pages < 0) return fail(PKV_INVALID_ARGUMENT, "negative page count");
+  if (waves < 1 || waves > (1 << 20)) return fail(PKV_INVALID_ARGUMENT, "waves must be in [1, 2^20]");
+  if (!out) return fail(PKV_INVALID_ARGUMENT, "read probe requires an output buffer");
+  if (count == 0) return PKV_OK;
+  if (!pool || !page_ids) return fail(PKV_INVALID_ARGUMENT, "read probe requires pool and ids");
+  return check_launch(pkv::launch_read_probe((hipStream_t)stream, (const uint8_t *)pool, num_pages,
+                                             geo.page_bytes, page_ids, count, waves, (uint32_t *)out),
+                      "read probe launch");
+}
+
 int pkv_quantize_rows(void *stream, const void *values, int64_t rows, int32_t dim, int32_t bits,
                       int32_t group_size, int32_t float_kind, void *codes, void *scale, void *bias) {
   if (bits != 4 && bits != 8) return fail(PKV_UNSUPPORTED, "paged quantization supports 4 or 8 bits");

@@ -128,6 +128,10 @@ hipError_t launch_quantize_rows(hipStream_t stream, const QuantRowsArgs &a);
 hipError_t launch_dequantize_rows(hipStream_t stream, const DequantRowsArgs &a);
 hipError_t launch_append(hipStream_t stream, const AppendArgs &a);
 hipError_t launch_gather(hipStream_t stream, const GatherArgs &a);
+// Streaming read of the listed pages (all heads) by `waves` one-wave
+// workgroups; out: waves * 64 words.
+hipError_t launch_read_probe(hipStream_t stream, const uint8_t *pool, int64_t num_pages, int64_t page_bytes,
+                             const int32_t *ids, int64_t count, int waves, uint32_t *out);
 hipError_t launch_copy(hipStream_t stream, uint8_t *pool, int64_t num_pages, int64_t page_bytes,
                        const int32_t *src, const int32_t *dst, int count);
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a);

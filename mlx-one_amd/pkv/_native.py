@@ -49,6 +49,7 @@ SIGNATURES = {
     "pkv_gather_pages": ([_c_p, _LP, _c_p, _i64, _c_p, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
                          ctypes.c_int),
     "pkv_copy_pages": ([_c_p, _LP, _c_p, _i64, _c_p, _c_p, _i32], ctypes.c_int),
+    "pkv_read_probe": ([_c_p, _LP, _c_p, _i64, _c_p, _i64, _i32, _c_p], ctypes.c_int),
     "pkv_quantize_rows": ([_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p],
                           ctypes.c_int),
     "pkv_dequantize_rows": ([_c_p, _c_p, _c_p, _c_p, _i64, _i32, _i32, _i32, _c_p],

@@ -146,6 +146,21 @@ def test_quantize_rows_argument_validation():
     assert lib.pkv_dequantize_rows(None, FAKE, FAKE, FAKE, 4, 0, 8, 32, FAKE) == nat.PKV_INVALID_ARGUMENT
 
 
+def test_read_probe_argument_validation():
+    lib = nat.load()
+    layout = _layout()
+    call = lambda **kw: lib.pkv_read_probe(None, kw.get("layout", layout), kw.get("pool", FAKE), 10,
+                                           kw.get("ids", FAKE), kw.get("count", 4),
+                                           kw.get("waves", 8), kw.get("out", FAKE))
+    assert call(waves=0) == nat.PKV_INVALID_ARGUMENT
+    assert call(count=-1) == nat.PKV_INVALID_ARGUMENT
+    assert call(out=None) == nat.PKV_INVALID_ARGUMENT
+    assert call(pool=None) == nat.PKV_INVALID_ARGUMENT
+    assert call(ids=None) == nat.PKV_INVALID_ARGUMENT
+    assert call(count=0) == nat.PKV_OK
+    assert call(layout=_layout(bits=3)) == nat.PKV_UNSUPPORTED
+
+
 def test_status_codes_map_to_reference_exceptions():
     from pkv.cache_errors import CacheCapacityError
     from pkv.modes import ModelCapabilityUnsupported
