@@ -69,7 +69,82 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <int BITS, int DP, int G, int FK>
+// Query rows of sequence b live in this launch: 0 for a sequence of a mixed
+// batch that the decode kernel serves (narrow_q > 0, width at most narrow_q).
+__device__ __forceinline__ int prefill_width(const AttnArgs &a, int b) {
+  return a.widths ? (a.narrow_q > 0 && a.widths[b] <= a.narrow_q ? 0 : a.widths[b]) : a.nq;
+}
+
+// The k-th (from 0) sequence, in batch order, whose rows are live here
+// (live) or not (!live); -1 past the last.  Uniform; the whole wave calls.
+__device__ int nth_sequence(const AttnArgs &a, bool live, int k, int lane) {
+  int carry = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int idx = c0 + lane;
+    const int f = idx < a.batch && ((prefill_width(a, idx) > 0) == live) ? 1 : 0;
+    const int incl = wave_scan_incl(f, lane) + carry;
+    const unsigned long long hit = __ballot(f && incl == k + 1);
+    if (hit) return c0 + __ffsll((long long)hit) - 1;
+    carry = __builtin_amdgcn_readlane(incl, 63);
+  }
+  return -1;
+}
+
+// Zeros into one output row of `dim` 16-bit elements (4-byte lanes where aligned).
+__device__ __forceinline__ void zero_row(uint16_t *o, int dim, int lane) {
+  for (int d = 2 * lane; d < dim; d += 128) {
+    if (d + 1 < dim && ((uintptr_t)(o + d) & 3) == 0) {
+      *(uint32_t *)(o + d) = 0u;
+    } else {
+      o[d] = 0;
+      if (d + 1 < dim) o[d + 1] = 0;
+    }
+  }
+}
+
+// A block's share [z, zend) of the dead rows of a mixed batch, in the
+// flattened space z = ((n * HK + kh) * gqa + hh) * nq + qi over the sequences
+// n that the decode kernel serves (in batch order): runs of consecutive qi
+// are contiguous in the output, and the block's `nthreads` threads fill each
+// run with 16-byte stores (rows whose bytes are not 16-byte multiples: a
+// wave per row).
+__device__ __forceinline__ void zero_share(const AttnArgs &a, int64_t z, int64_t zend, int tid,
+                                                     int nthreads) {
+  const int lane = tid & 63, wv = tid >> 6, nwaves = nthreads >> 6;
+  const int64_t per_seq = (int64_t)a.g.hk * a.rows;
+  int n = (int)(z / per_seq);
+  const int64_t r = z % per_seq;
+  int kh = (int)(r / a.rows);
+  const int r2 = (int)(r % a.rows);
+  int hh = r2 / a.nq, qi = r2 % a.nq;
+  int b = nth_sequence(a, false, n, lane);
+  const int dim = a.g.dim;
+  const bool vec = (dim & 7) == 0 && ((uintptr_t)a.out & 15) == 0;
+  while (z < zend && b >= 0) {
+    const int run = (int)min((int64_t)(a.nq - qi), zend - z);
+    uint16_t *o = a.out + (((int64_t)b * a.heads + kh * a.gqa + hh) * a.nq + qi) * dim;
+    if (vec) {
+      const int units = run * (dim / 8);
+      for (int u = tid; u < units; u += nthreads) ((u4 *)o)[u] = u4{0, 0, 0, 0};
+    } else {
+      for (int i = wv; i < run; i += nwaves) zero_row(o + (int64_t)i * dim, dim, lane);
+    }
+    z += run;
+    qi += run;
+    if (qi == a.nq) {
+      qi = 0;
+      if (++hh == a.gqa) {
+        hh = 0;
+        if (++kh == a.g.hk) {
+          kh = 0;
+          b = nth_sequence(a, false, ++n, lane);
+        }
+      }
+    }
+  }
+}
+
+template <int BITS, int DP, int G, int FK, bool SHARE>
 __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const AttnArgs a) {
   constexpr int kPrefillWaves = prefill_waves(DP);
   constexpr int kStageTiles = kPrefillWaves;
@@ -84,6 +159,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 
   __shared__ __attribute__((aligned(16))) int s_valid[2][kStageTiles];
   __shared__ int s_lim[2][kPrefillWaves];
+  __shared__ int64_t s_zero[SHARE ? 2 : 1];  // zero share: first row, end
   __shared__ __attribute__((aligned(16))) uint16_t stage[2][I::ELEMS];
 
   const int tid = threadIdx.x;
@@ -91,24 +167,65 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, jj = lane >> 4;
   const Geo &g = a.g;
-  // Blocks of one (sequence, KV head) read the same pages: give them
-  // consecutive slots of one XCD (workgroups are dealt to the 8 XCDs
+  // Work items.  Blocks of one (sequence, KV head) read the same pages: give
+  // them consecutive slots of one XCD (workgroups are dealt to the 8 XCDs
   // round-robin) so the span is fetched into one L2.  XCD x runs segments
-  // x, x + 8, x + 16, ...: heavy segments that sit together in the batch (the
-  // prefill rows of a mixed batch) still spread over every XCD.
+  // x, x + 8, x + 16, ...: heavy segments that sit together in the batch still
+  // spread over every XCD.
+  //
+  // A mixed batch's sequences that the decode kernel serves (width 0 here)
+  // only need zeros in their rows (the decode kernel, launched next, writes
+  // the rows it serves).  Their blocks would each hold a CU (and its LDS)
+  // for a few stores and delay the blocks with work behind them, so the
+  // first R blocks of the grid take the R blocks of the sequences with live
+  // rows, in order, and also write those zeros (an equal share each, after
+  // their own rows: blocks of different causal spans end at different
+  // times), and the rest of the grid exits at once.
+  // (SHARE: the instantiation for mixed batches, launched when the decode
+  // kernel serves some of the call's sequences; others carry none of it.)
   const int nblk = (a.rows + ROWS - 1) / ROWS;
   int bid = blockIdx.x;
-  if (((gridDim.x / nblk) & 7) == 0) {
+  int64_t zlo = 0, zhi = 0;  // zero rows (of the flattened dead-row space) this block writes
+  bool share = false;
+  int R = (int)gridDim.x;
+  if constexpr (SHARE) {
+    int nlive = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int idx = c0 + lane;
+      nlive += wave_sum(idx < a.batch && prefill_width(a, idx) > 0 ? 1 : 0);
+    }
+    share = nlive > 0 && nlive < a.batch;
+    if (share) {
+      R = nlive * g.hk * nblk;
+      if (bid >= R) return;
+      const int64_t Z = (int64_t)(a.batch - nlive) * g.hk * a.rows;
+      zlo = (int64_t)bid * Z / R;
+      zhi = (int64_t)(bid + 1) * Z / R;
+    }
+  }
+  const int span = R;
+  if (((span / nblk) & 7) == 0) {
     const int x = bid & 7, k = bid >> 3;
     bid = (x + 8 * (k / nblk)) * nblk + k % nblk;
   }
   const int seg = bid / nblk, rblk = bid % nblk;
-  const int b = seg / g.hk, kh = seg % g.hk;
-  if (b >= a.batch) return;
+  const int b = share ? nth_sequence(a, true, seg / g.hk, lane) : seg / g.hk;
+  const int kh = seg % g.hk;
+  if (b < 0 || b >= a.batch) return;
   const int L = a.seq_lens[b];
-  // a sequence of a mixed batch that the decode kernel serves: zeros here,
-  // its rows are written by the decode kernel launched next on the stream
-  const int width = a.widths ? (a.narrow_q > 0 && a.widths[b] <= a.narrow_q ? 0 : a.widths[b]) : a.nq;
+  const int width = prefill_width(a, b);
+  if (SHARE && width <= 0) {
+    // no row of this sequence is live here (every sequence of the call is
+    // left to the decode kernel): the block's rows are zeros, written
+    // without the query loads and the span walk (elsewhere such rows take
+    // the general path: limit -1, zero output)
+    const int r0 = rblk * ROWS, r1 = min(a.rows, r0 + ROWS);
+    for (int row = r0 + wv; row < r1; row += kPrefillWaves) {
+      const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
+      zero_row(a.out + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim, g.dim, lane);
+    }
+    return;
+  }
 
   // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];
@@ -199,6 +316,10 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       s_lim[0][wv] = hi;
       s_lim[1][wv] = lo;
     }
+  }
+  if (SHARE && tid == 0) {
+    s_zero[0] = zlo;
+    s_zero[1] = zhi;
   }
   __syncthreads();
   int tmax = -1, tmin = 0x7FFFFFFF;
@@ -555,15 +676,22 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       }
     }
   }
+  // the block's share of the dead sequences' zero rows, after its own output
+  // rows (stores issued before the stages would hold up the first tile
+  // loads: vmcnt counts both, in order)
+  if constexpr (SHARE) {
+    if (share) zero_share(a, s_zero[0], s_zero[1], tid, 64 * kPrefillWaves);
+  }
 }
 
 // ---- host launcher ------------------------------------------------------------
 
 typedef void (*PrefillKernel)(AttnArgs);
 
+template <bool SHARE>
 static PrefillKernel select_prefill(const Geo &g) {
 #define PKV_Q(BITS_, DP_, G_) \
-  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return prefill_kernel<BITS_, DP_, G_, 1>;
+  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return prefill_kernel<BITS_, DP_, G_, 1, SHARE>;
   PKV_Q(8, 64, 32) PKV_Q(8, 64, 64)
   PKV_Q(8, 128, 32) PKV_Q(8, 128, 64) PKV_Q(8, 128, 128)
   PKV_Q(8, 256, 32) PKV_Q(8, 256, 64) PKV_Q(8, 256, 128)
@@ -572,14 +700,15 @@ static PrefillKernel select_prefill(const Geo &g) {
   PKV_Q(4, 256, 32) PKV_Q(4, 256, 64) PKV_Q(4, 256, 128)
 #undef PKV_Q
 #define PKV_F(DP_, FK_) \
-  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_) return prefill_kernel<16, DP_, 32, FK_>;
+  if (g.bits == 16 && g.dp == DP_ && g.float_kind == FK_) return prefill_kernel<16, DP_, 32, FK_, SHARE>;
   PKV_F(64, 0) PKV_F(64, 1) PKV_F(128, 0) PKV_F(128, 1) PKV_F(256, 0) PKV_F(256, 1)
 #undef PKV_F
   return nullptr;
 }
 
 hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a) {
-  const PrefillKernel k = select_prefill(a.g);
+  // sequences left to the decode kernel: the instantiation that shares their zero rows out
+  const PrefillKernel k = a.widths && a.narrow_q > 0 ? select_prefill<true>(a.g) : select_prefill<false>(a.g);
   if (!k) return hipErrorInvalidValue;
   const int rows_per_block = prefill_rows(a.g.dp);
   const int64_t blocks = (int64_t)a.batch * a.g.hk * ((a.rows + rows_per_block - 1) / rows_per_block);
