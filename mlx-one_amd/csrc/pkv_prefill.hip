@@ -106,8 +106,11 @@ __device__ __forceinline__ void zero_row(uint16_t *o, int dim, int lane) {
 // flattened space z = ((n * HK + kh) * gqa + hh) * nq + qi over the sequences
 // n that the decode kernel serves (in batch order): runs of consecutive qi
 // are contiguous in the output, and the block's `nthreads` threads fill each
-// run with 16-byte stores (rows whose bytes are not 16-byte multiples: a
-// wave per row).
+// run with 16-byte non-temporal stores (rows whose bytes are not 16-byte
+// multiples: a wave per row).  Non-temporal, so that the zeros reach HBM
+// while this MFMA-bound kernel leaves it idle instead of lingering in the
+// memory-side cache to be written back under the decode kernel that follows
+// (its launch: 88 -> 69 us in a mixed C2 + C5 batch).
 __device__ __forceinline__ void zero_share(const AttnArgs &a, int64_t z, int64_t zend, int tid,
                                                      int nthreads) {
   const int lane = tid & 63, wv = tid >> 6, nwaves = nthreads >> 6;
@@ -125,7 +128,7 @@ __device__ __forceinline__ void zero_share(const AttnArgs &a, int64_t z, int64_t
     uint16_t *o = a.out + (((int64_t)b * a.heads + kh * a.gqa + hh) * a.nq + qi) * dim;
     if (vec) {
       const int units = run * (dim / 8);
-      for (int u = tid; u < units; u += nthreads) ((u4 *)o)[u] = u4{0, 0, 0, 0};
+      for (int u = tid; u < units; u += nthreads) __builtin_nontemporal_store(u4{0, 0, 0, 0}, (u4 *)o + u);
     } else {
       for (int i = wv; i < run; i += nwaves) zero_row(o + (int64_t)i * dim, dim, lane);
     }
