@@ -316,6 +316,11 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   using C = Cfg<BITS, DP, G, RB, FK, SLOTS>;
   constexpr bool QUANT = C::QUANT;
   static_assert(!APPEND || (QUANT && RB == 1), "fused append: quantized pages, one row block");
+  // Tiles stream in with non-temporal loads for one row block (decode rows:
+  // C2 67.7 -> 59.9 us per fused launch); two row blocks (verify) keep plain
+  // loads, which let the sequences of a shared prefix meet its pages in L2
+  // (C4: 32.8 against 33.8 us with non-temporal loads).
+  constexpr bool NT = RB == 1;
   constexpr int NG = C::NG, KB = C::KB, NB = C::NB, RPS = C::RPS;
   // MFMA operand types: quantized pages run in f16 (codes as 1024 + c).
   using FO = FloatOps<QUANT ? 1 : FK>;
@@ -584,14 +589,14 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   auto load_k = [&](int pkh, const int (&pg)[SLOTS], const int (&tp)[SLOTS], const uint8_t *mp)
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < SLOTS; ++j) load_payload<C>(kw[j], tile_at(pkh, pg[j], tp[j]), lane);
-    if constexpr (QUANT) load_meta<C>(km, mp);
+    for (int j = 0; j < SLOTS; ++j) load_payload<C, NT>(kw[j], tile_at(pkh, pg[j], tp[j]), lane);
+    if constexpr (QUANT) load_meta<C, NT>(km, mp);
   };
   auto load_v = [&](int pkh, const int (&pg)[SLOTS], const int (&tp)[SLOTS], const uint8_t *mp)
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < SLOTS; ++j) load_payload<C>(vw[j], tile_at(pkh, pg[j], tp[j]) + g.v_offset, lane);
-    if constexpr (QUANT) load_meta<C>(vm, mp);
+    for (int j = 0; j < SLOTS; ++j) load_payload<C, NT>(vw[j], tile_at(pkh, pg[j], tp[j]) + g.v_offset, lane);
+    if constexpr (QUANT) load_meta<C, NT>(vm, mp);
   };
 
   // ---- pieces.  Current: tiles [cta, ctb) of segment (cb, ckh) starting at

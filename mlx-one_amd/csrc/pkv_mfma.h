@@ -40,26 +40,32 @@ struct Cfg {
 };
 
 // A lane's K or V payload of one tile, straight from HBM.
-template <typename C>
+// NT: non-temporal loads (streamed once: the decode kernels, whose pages are
+// read by one wave each); the prefill kernel's row blocks share a span's
+// tiles through L2 and load them plainly.
+template <typename C, bool NT = false>
 __device__ __forceinline__ void load_payload(uint32_t (&w)[C::LW], const uint8_t *tile, int lane) {
   if constexpr (C::CS == 16) {
 #pragma unroll
     for (int c = 0; c < C::NCH; ++c) {
-      const u4 x = *(const u4 *)(tile + c * 1024 + lane * 16);
+      const u4 *src = (const u4 *)(tile + c * 1024 + lane * 16);
+      const u4 x = NT ? __builtin_nontemporal_load(src) : *src;
       w[4 * c] = x.x; w[4 * c + 1] = x.y; w[4 * c + 2] = x.z; w[4 * c + 3] = x.w;
     }
   } else {
-    const u2 x = *(const u2 *)(tile + lane * 8);
+    const u2 *src = (const u2 *)(tile + lane * 8);
+    const u2 x = NT ? __builtin_nontemporal_load(src) : *src;
     w[0] = x.x; w[1] = x.y;
   }
 }
 
 // The metadata words (all groups) of a lane's four tokens: 4*NG contiguous dwords.
-template <typename C>
+template <typename C, bool NT = false>
 __device__ __forceinline__ void load_meta(uint32_t (&mw)[C::MW], const uint8_t *p) {
 #pragma unroll
   for (int i = 0; i < C::MW; i += 4) {
-    const u4 x = *(const u4 *)(p + i * 4);
+    const u4 *src = (const u4 *)(p + i * 4);
+    const u4 x = NT ? __builtin_nontemporal_load(src) : *src;
     mw[i] = x.x; mw[i + 1] = x.y; mw[i + 2] = x.z; mw[i + 3] = x.w;
   }
 }

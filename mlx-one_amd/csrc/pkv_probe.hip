@@ -3,8 +3,8 @@
 //
 // Wave w of W reads pages [w*n/W, (w+1)*n/W) of a page-id list in order, every
 // byte of each page (all KV heads) as 16-byte loads, 16 per lane in flight
-// (16 KiB per wave), and folds them into one word per lane so that the loads
-// cannot be dropped.  Given the pages a decode step's sequences hold, in
+// (16 KiB per wave), non-temporal like the decode kernel's tile loads, and
+// folds them into one word per lane so that the loads cannot be dropped.  Given the pages a decode step's sequences hold, in
 // block-table order, and the decode launch's wave count, it moves the step's
 // KV bytes with nothing but the loads: what HBM delivers for that access
 // pattern on this device.
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(64) void read_probe_kernel(const uint8_t *__restric
 #pragma unroll
       for (int k = 0; k < kInFlight; ++k) {
         const int64_t u = u0 + k * 64 + lane;
-        v[k] = u < units ? base[u] : u4v{0, 0, 0, 0};
+        v[k] = u < units ? __builtin_nontemporal_load(base + u) : u4v{0, 0, 0, 0};
       }
 #pragma unroll
       for (int k = 0; k < kInFlight; ++k) acc ^= v[k];
