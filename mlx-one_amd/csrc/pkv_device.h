@@ -76,7 +76,9 @@ __device__ __forceinline__ int v4_byte(int r) {
 // Wave-wide inclusive prefix sum on DPP moves (no LDS round trips): prefix
 // sums within each 16-lane row by row_shr 1, 2, 4, 8 (lanes shifted in from
 // before the row read 0), then row 1 and row 3 add lane 15 / 47
-// (row_bcast:15), rows 2 and 3 add lane 31 (row_bcast:31).  `lane` is unused.
+// (row_bcast:15), rows 2 and 3 add lane 31 (row_bcast:31).  The whole wave
+// calls it with every lane active (a DPP read of a disabled lane gives 0).
+// `lane` is unused.
 __device__ __forceinline__ int wave_scan_incl(int v, int /*lane*/) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
   v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
