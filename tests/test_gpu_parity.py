@@ -363,6 +363,14 @@ MIXED_CASES = {
     "bf16_pages_many_decode": dict(name="c5", batch=70, lengths=(), length_range=(1, 600),
                                    num_queries=48, append_tokens=48, bits=16,
                                    widths=(48, 1, 2, 3, 7) * 14),
+    # head_dim 100: the prefill blocks write the decode rows' zeros row by row
+    # (rows of 200 bytes are not 16-byte multiples)
+    "d100_zero_rows_by_row": dict(name="c5", batch=5, lengths=(60, 400, 20, 9, 250), head_dim=100,
+                                  group_size=32, num_queries=40, append_tokens=40,
+                                  widths=(1, 40, 2, 1, 33)),
+    # every sequence narrow: no prefill row is live, each block zeroes its own rows
+    "all_rows_decode_padded": dict(name="c5", batch=4, lengths=(70, 300, 15, 128), num_queries=40,
+                                   append_tokens=40, widths=(1, 2, 8, 3)),
 }
 
 
