@@ -80,6 +80,9 @@ constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
              : 1;
 }
 
+// Quantized tiles of two-row-block kernels dequantized in registers (see attn_kernel).
+constexpr bool kDequantRows = true;
+
 // Tiles of a sequence: at least one, so that an empty sequence still owns a
 // piece that writes its zero output.
 __device__ __forceinline__ int seq_tiles(int len) {
@@ -321,6 +324,16 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   // loads, which let the sequences of a shared prefix meet its pages in L2
   // (C4: 32.8 against 33.8 us with non-temporal loads).
   constexpr bool NT = RB == 1;
+  // Quantized V tiles for two row blocks (17-32 query rows per KV head) are
+  // dequantized once per tile in registers -- per lane its four tokens,
+  // (c - 1024)*scale + bias in f16 as the prefill kernel does -- and the PV
+  // contraction takes P itself: with 20 rows the per-group P' operands and
+  // bias sums of the undequantized form (AFF) cost more VALU than the
+  // elements' conversion.  K stays undequantized at every shape (codes exact
+  // in the MFMA, scales applied to the f32 scores), which keeps queries far
+  // past unit scale within the bar.
+  constexpr bool DEQ = QUANT && RB == 2 && kDequantRows;
+  constexpr bool AFF = QUANT && !DEQ;
   constexpr int NG = C::NG, KB = C::KB, NB = C::NB, RPS = C::RPS;
   // MFMA operand types: quantized pages run in f16 (codes as 1024 + c).
   using FO = FloatOps<QUANT ? 1 : FK>;
@@ -780,7 +793,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     // term) and osum4 = sum P' (the 1024 offset), as 16x16x16 products of the
     // tokens' f16 biases (or ones) with p (or P'); every row of the result
     // holds the column's sum.
-    constexpr bool MSUM = RB == 2 && QUANT;
+    constexpr bool MSUM = RB == 2 && AFF;
     f4 csum[MSUM ? RB : 1][MSUM ? NG : 1], osum4[MSUM ? RB : 1][MSUM ? NG : 1];
     f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
 #pragma unroll
@@ -918,7 +931,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             if constexpr (MSUM) {
               csum[rb][gi] *= alpha;
               osum4[rb][gi] *= alpha;
-            } else {
+            } else if constexpr (AFF) {
               corr[rb][gi] *= alpha;
               osum[rb][gi] *= alpha;
             }
@@ -952,7 +965,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
         for (int r = 0; r < 4; ++r) p[r] = vis[rb][r] ? __builtin_amdgcn_exp2f(s[rb][r] - m[rb]) : 0.0f;
         lsum[rb] += (p[0] + p[1]) + (p[2] + p[3]);
-        if constexpr (QUANT) {
+        if constexpr (AFF) {
 #pragma unroll
           for (int gi = 0; gi < NG; ++gi) {
             h4 pv;
@@ -1013,13 +1026,32 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
           for (int n = 0; n < NB; ++n) {
             VT vop;
-            if constexpr (QUANT) {
+            if constexpr (DEQ) {
+              // the lane's four tokens 4jj..4jj+3 of column 16n + col,
+              // dequantized; tokens past the piece's end (stale metadata) zero
+              const int gi = (16 * n) / G;
+              h4 sc, bi;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const h2 sb = __builtin_bit_cast(h2, vm[r * NG + gi]);
+                sc[r] = sb.x;
+                bi[r] = sb.y;
+              }
+              const h4 c = Conv<BITS>::template vop<C::LW>(vw[j], n);
+              u2 x = __builtin_bit_cast(u2, __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi));
+              if (tail_it) {
+                const int tb = t0 + (it * SLOTS + j) * PKV_TILE + 4 * jj;
+                x.x &= (tb < t1 ? 0x0000FFFFu : 0u) | (tb + 1 < t1 ? 0xFFFF0000u : 0u);
+                x.y &= (tb + 2 < t1 ? 0x0000FFFFu : 0u) | (tb + 3 < t1 ? 0xFFFF0000u : 0u);
+              }
+              vop = __builtin_bit_cast(VT, x);
+            } else if constexpr (QUANT) {
               vop = Conv<BITS>::template vop<C::LW>(vw[j], n);
             } else {
               u2 r = {vw[j][2 * n], vw[j][2 * n + 1]};
               vop = __builtin_bit_cast(VT, r);
             }
-            const int gi = QUANT ? (16 * n) / G : 0;
+            const int gi = AFF ? (16 * n) / G : 0;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
               O[rb][n] = FO::pv(vop, bop[rb][gi], O[rb][n]);
@@ -1053,7 +1085,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         if constexpr (MSUM) {  // already summed over the tokens of every lane
           corr[rb][gi] = csum[rb][gi][0];
           osum[rb][gi] = osum4[rb][gi][0];
-        } else {
+        } else if constexpr (AFF) {
           corr[rb][gi] = xor32_add(xor16_add(corr[rb][gi]));
           osum[rb][gi] = xor32_add(xor16_add(osum[rb][gi]));
         }
@@ -1080,7 +1112,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float v = O[rb][n][r];
-          if constexpr (QUANT) {
+          if constexpr (AFF) {
             const int gi = (16 * n) / G;
             v += corr[rb][gi] - 1024.0f * osum[rb][gi];
           }
