@@ -80,7 +80,7 @@ constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
              : 1;
 }
 
-// Quantized tiles of two-row-block kernels dequantized in registers (see attn_kernel).
+// Two-row-block kernels dequantize quantized V tiles in registers (see attn_kernel).
 constexpr bool kDequantRows = true;
 
 // Tiles of a sequence: at least one, so that an empty sequence still owns a

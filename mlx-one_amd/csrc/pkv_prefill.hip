@@ -112,7 +112,7 @@ __device__ __forceinline__ void zero_row(uint16_t *o, int dim, int lane) {
 // memory-side cache to be written back under the decode kernel that follows
 // (its launch: 88 -> 69 us in a mixed C2 + C5 batch).
 __device__ __forceinline__ void zero_share(const AttnArgs &a, int64_t z, int64_t zend, int tid,
-                                                     int nthreads) {
+                                           int nthreads) {
   const int lane = tid & 63, wv = tid >> 6, nwaves = nthreads >> 6;
   const int64_t per_seq = (int64_t)a.g.hk * a.rows;
   int n = (int)(z / per_seq);
