@@ -299,7 +299,9 @@ def test_attention_takes_transposed_query_views(nq):
 
 @pytest.mark.parametrize("bits,nq,dtype", [(16, 1, "bfloat16"), (16, 5, "bfloat16"),
                                            (16, 2, "float16"), (8, 1, "bfloat16"),
-                                           (4, 3, "bfloat16")])
+                                           (4, 3, "bfloat16"),
+                                           # two row blocks: V dequantized in registers
+                                           (8, 5, "bfloat16"), (4, 6, "bfloat16")])
 def test_attention_ignores_stale_bytes_of_reused_pages(bits, nq, dtype):
     """Pages handed out again still hold their last owner's bytes past the new
     sequence's end; here every byte starts as 0xFF (NaN for float pages,
