@@ -81,6 +81,13 @@ CASES = {
     "int4_d64_p64": (dict(name="c2", batch=3, lengths=(129, 64, 5), bits=4, head_dim=64,
                           group_size=32, page_tokens=64), 0),
     "b80_chunks": (dict(name="c2", batch=80, length_range=(1, 300)), 37),
+    "int8_d256_g128": (dict(name="c2", batch=3, lengths=(300, 17, 90), head_dim=256,
+                            group_size=128), 0),
+    "int8_d256_g32_gqa8": (dict(name="c2", batch=3, lengths=(129, 2, 48), head_dim=256,
+                                group_size=32, kv_heads=4), 5),
+    "int4_d256_g64_p32": (dict(name="c3", batch=2, lengths=(200, 45), head_dim=256), 0),
+    "int8_g128_gqa8_p64": (dict(name="c2", batch=4, lengths=(64, 65, 500, 3), kv_heads=4,
+                                group_size=128, page_tokens=64), 0),
     # served by two launches inside the entry point
     "fallback_bf16_pages": (dict(name="c2", batch=3, lengths=(40, 3, 70), bits=16,
                                  group_size=32), 0),
