@@ -97,9 +97,37 @@ CASES = {
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_fused_step_equals_append_then_attend(case):
+    overrides, waves = CASES[case]
+    _fused_against_separate(overrides, waves)
+
+
+# head_dim -> quantization groups the page format supports there
+_GROUPS = {64: (32, 64), 100: (32,), 128: (32, 64, 128), 256: (32, 64, 128)}
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_fused_step_random_shapes(seed):
+    """Seeded random single-token steps over the shapes the fused launch
+    serves (4 or 8 bits, head_dim 64/100/128/256 with their groups, pages of
+    16-64 tokens, 1-8 query heads per KV head, ragged lengths from 1 token,
+    default and odd wave counts), each checked as the fixed cases are."""
+    rng = np.random.default_rng(1000 + seed)
+    dim = int(rng.choice(list(_GROUPS)))
+    kv = int(rng.choice([1, 2, 4, 8]))
+    batch = int(rng.integers(1, 13))
+    overrides = dict(name="c2", batch=batch, bits=int(rng.choice([4, 8])), head_dim=dim,
+                     group_size=int(rng.choice(_GROUPS[dim])),
+                     page_tokens=int(rng.choice([16, 32, 64])), kv_heads=kv,
+                     heads=kv * int(rng.choice([1, 2, 4, 8])),
+                     lengths=tuple(int(x) for x in rng.integers(1, 1500, size=batch)))
+    waves = int(rng.choice([0, 0, 1, 3, 17, 64]))
+    print(f"seed {seed}: {overrides}, waves {waves}", flush=True)
+    _fused_against_separate(overrides, waves)
+
+
+def _fused_against_separate(overrides, waves):
     from pkv import ops, workloads
 
-    overrides, waves = CASES[case]
     overrides = dict(overrides)
     w = workloads.get(overrides.pop("name"), num_queries=1, append_tokens=1,
                       shared_prefix_pages=0, **overrides)
