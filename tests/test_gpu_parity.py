@@ -383,9 +383,40 @@ def test_mixed_batch_routes_rows_per_sequence(case):
     prefill kernel; both against the oracle, padded rows zero.  With no room
     for the decode part's partials, the prefill kernel serves every sequence
     (same result within the bar)."""
+    _check_mixed(MIXED_CASES[case])
+
+
+_MIXED_GROUPS = {64: (32, 64), 128: (32, 64, 128), 256: (32, 64, 128)}
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_mixed_batch_random(seed):
+    """Seeded random mixed batches: 4-bit, int8 or bf16 pages, head_dim
+    64/128/256, pages of 16-64 tokens, 1-8 query heads per KV head, and per
+    sequence a width from 1 token up to a prefill chunk (at least one chunk
+    wide enough for the prefill kernel), each checked as the fixed cases are."""
+    rng = np.random.default_rng(2000 + seed)
+    dim = int(rng.choice(list(_MIXED_GROUPS)))
+    bits = int(rng.choice([4, 8, 16]))
+    kv = int(rng.choice([1, 2, 4, 8]))
+    gqa = int(rng.choice([1, 2, 4, 8]))
+    batch = int(rng.integers(2, 9))
+    q = int(rng.integers(33 // gqa + 1, 97))
+    widths = [int(x) for x in rng.choice([1, 1, 2, 3, 5, 8, 17, q], size=batch)]
+    widths[int(rng.integers(0, batch))] = q
+    overrides = dict(name="c5", batch=batch, bits=bits, head_dim=dim,
+                     group_size=32 if bits == 16 else int(rng.choice(_MIXED_GROUPS[dim])),
+                     page_tokens=int(rng.choice([16, 32, 64])), kv_heads=kv, heads=kv * gqa,
+                     lengths=tuple(int(x) for x in rng.integers(1, 800, size=batch)),
+                     num_queries=q, append_tokens=q, widths=tuple(widths))
+    print(f"seed {seed}: {overrides}", flush=True)
+    _check_mixed(overrides)
+
+
+def _check_mixed(overrides):
     from pkv import ops, workloads
 
-    overrides = dict(MIXED_CASES[case])
+    overrides = dict(overrides)
     w = workloads.get(overrides.pop("name"), **overrides)
     inst = workloads.generate(w)
     fmt = _fmt(w)
