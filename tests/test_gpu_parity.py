@@ -596,14 +596,16 @@ def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays():
 
 
 
-def _random_attention_cases(count, seed):
+def _random_attention_cases(count, seed, dims=(64, 128, 128, 100), groups=(32, 64), prefix=""):
     """Seeded random decode/verify cases across the decode kernel's shapes."""
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(count):
         bits = int(rng.choice([4, 8, 8, 16]))
-        dim = int(rng.choice([64, 128, 128, 100]))
-        group = int(rng.choice([32, 64])) if bits != 16 else 32
+        dim = int(rng.choice(dims))
+        group = int(rng.choice(groups)) if bits != 16 else 32
+        if bits != 16 and group > dim:
+            group = 32
         if bits != 16 and -(-dim // group) * group not in (64, 128, 256):
             group = 32
         page = int(rng.choice([16, 32, 64]))
@@ -619,7 +621,7 @@ def _random_attention_cases(count, seed):
         cases.append(dict(bits=bits, head_dim=dim, group_size=group, page_tokens=page,
                           kv_heads=kv_heads, heads=kv_heads * gqa, num_queries=nq,
                           append_tokens=nq, batch=batch, lengths=lengths, waves=waves,
-                          seed=int(rng.integers(1 << 30)), index=i))
+                          seed=int(rng.integers(1 << 30)), index=f"{prefix}{i}"))
     return cases
 
 
@@ -633,7 +635,11 @@ _RANDOM_REGRESSIONS = [
 ]
 
 
-@pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026) + _RANDOM_REGRESSIONS,
+# a second set with head_dim 256 and G128 (head_dim 256 past 16 rows per KV
+# head runs on the prefill kernel)
+@pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026) + _RANDOM_REGRESSIONS
+                         + _random_attention_cases(32, seed=2027, dims=(64, 128, 256, 256),
+                                                   groups=(32, 64, 128), prefix="w"),
                          ids=lambda c: f"r{c['index']}")
 def test_attention_random_shapes_match_oracle(case):
     """Random layouts (4/8-bit G32/G64 and bf16 pages, D 64-128, pages of
