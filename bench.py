@@ -295,7 +295,9 @@ def layer_bench(args):
     libpkv, output projection) for C2's batch and context lengths, q8_0 KV
     (f16 activations, as the reference's CacheManager pairs q8_0 with f16).
     Contexts are prefilled through the runner in 1,024-token chunks before
-    timing; each timed step is one runner call (host bookkeeping included)."""
+    timing; each timed step is one runner call (host bookkeeping included).
+    This is ``--workload layer --arena host``; the default is the device
+    arena (``layer_device_bench``)."""
     import numpy as np
     import torch
 
@@ -373,10 +375,11 @@ def layer_device_bench(args):
     (``CacheManager.create_handle`` + ``PagedRunner.execute``) with the page
     bookkeeping on the device: ``CacheConfig(page_arena="device")`` gives each
     handle a ``DevicePageArena`` slot, so a step is one reservation kernel
-    instead of per-sequence host page tables.  With ``--graph`` the runner
+    instead of per-sequence host page tables.  Unless ``--eager``, the runner
     replays repeated decode steps of the same sequences as captured HIP graphs
     (reservation, then QKV GEMM, RoPE, append, attention, merge, output GEMM),
-    reading the reservation's error bits between the two."""
+    reading the reservation's error bits between the two.  ``--arena host``
+    runs the same steps with host page tables (``layer_bench``)."""
     import numpy as np
     import torch
 
@@ -405,7 +408,7 @@ def layer_device_bench(args):
                       device=device)
     handles = [cm.create_handle(f"seq{b}", key_type="q8_0", value_type="q8_0")
                for b in range(w.batch)]
-    runner = PagedRunner(model, graphs=bool(args.graph))
+    runner = PagedRunner(model, graphs=not args.eager)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
 
@@ -446,7 +449,7 @@ def layer_device_bench(args):
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "layer", "arena": "device", "graph": bool(args.graph),
+        "config": {"workload": "layer", "arena": "device", "graph": not args.eager,
                    "batch": w.batch, "hidden": spec.hidden, "heads": spec.query_heads,
                    "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "kv": "q8_0",
                    "group_size": w.group_size, "page_tokens": w.page_tokens,
@@ -516,17 +519,18 @@ def main(argv=None):
                         help="kernel for decode rows (<= 4 query rows per KV head, quantized "
                              "pages): the MFMA form (default) or the vector-ALU form")
     parser.add_argument("--graph", action="store_true",
-                        help="layer workload: replay each decode step as a captured HIP graph "
-                             "(the attention workloads replay their timed steps as one graph "
-                             "unless --eager)")
+                        help="kept for older command lines: graph replay is the default "
+                             "(--eager turns it off)")
     parser.add_argument("--eager", action="store_true",
-                        help="attention workloads: launch each timed step from the host instead "
-                             "of replaying them as one captured HIP graph")
+                        help="launch each timed step from the host instead of replaying "
+                             "captured HIP graphs (attention workloads: the timed steps as one "
+                             "graph; layer workload on the device arena: each decode step)")
     parser.add_argument("--cpu-budget", type=float, default=15.0,
                         help="seconds of CPU baseline timing (0 disables)")
-    parser.add_argument("--arena", choices=("host", "device"), default="host",
-                        help="layer workload: page bookkeeping on the host (PagedRunner) or "
-                             "the device (DeviceRunner)")
+    parser.add_argument("--arena", choices=("host", "device"), default="device",
+                        help="layer workload: page bookkeeping on the device (CacheManager with "
+                             "page_arena=\"device\", the default) or on the host (host page "
+                             "tables per sequence)")
     parser.add_argument("--copy-probe", action="store_true",
                         help="only run three 256 MiB device copies (calibrates rocprofv3 "
                              "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic)")
