@@ -314,8 +314,10 @@ int pkv_arena_init(void *stream, void *state, int32_t capacity_pages);
  * a row only up to its length), batch_starts [count] (length before),
  * batch_lens [count] (length after).  If the free pages do not cover the call,
  * no slot grows, PKV_ARENA_OUT_OF_PAGES is set, and each growing slot's batch
- * row holds -1 from the page its first new token would go to (an append then
- * writes nothing).
+ * length is 0 and its batch row holds -1 from the page its first new token
+ * would go to: an append positioned by batch_starts or by batch_lens (the
+ * single-token pkv_append_paged_attention) then writes nothing, and no cached
+ * token is overwritten.  A slot whose table is full is blocked the same way.
  */
 int pkv_arena_reserve(void *stream, void *state, int32_t capacity_pages, int32_t page_tokens,
                       int32_t *slot_table, int32_t num_slots, int32_t max_pages, int32_t *slot_lens,

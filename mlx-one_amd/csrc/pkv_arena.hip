@@ -72,8 +72,9 @@ __global__ void arena_init_kernel(int32_t *state, int capacity) {
 // The batch row of slot i gets the slot's page ids (entries past them are not
 // written: the kernels read a row only up to its length).  A slot that cannot
 // grow (its table is full, or the stack is short -- then no slot of the chunk
-// grows) keeps its length, and its batch row holds -1 from the page its first
-// new token would go to, so an append writes nothing.
+// grows) keeps its length, its batch length is 0 and its batch row holds -1
+// from the page its first new token would go to, so no append (positioned by
+// the start or by the batch length) writes anything.
 //
 // Order of work, to overlap the dependent memory round trips: lengths and tail
 // page ids; the copy of each row's existing entries (in flight while) the
@@ -207,8 +208,13 @@ __global__ __launch_bounds__(kThreads) void arena_reserve_kernel(ArenaArgs a) {
       for (int p = L / P; p < min(mp, cdiv(L + w, P)); ++p) a.batch_table[brow + p] = -1;
     }
     if (i < a.count) {
+      // A row that cannot grow reports length 0: a single-token append puts
+      // its token at lens - 1, which for the old length L would be the last
+      // cached token (a valid, possibly shared page when L % P == 0).  With 0
+      // the append writes nothing and the attention reads nothing; the host
+      // raises on the error bit and discards the step's output.
       a.batch_starts[i] = L;
-      a.batch_lens[i] = nl;
+      a.batch_lens[i] = blocked && w > 0 ? 0 : nl;
     }
     __syncthreads();
     if (threadIdx.x == 0 && !s_fail) s_top = top - total;

@@ -140,6 +140,67 @@ def test_out_of_pages_and_full_table_change_nothing():
     assert arena.lens[0].item() == 31
 
 
+def test_a_blocked_decode_step_overwrites_no_cached_token():
+    """Regression: slots whose length is a multiple of the page size (one of
+    them sharing forked pages) and no free page.  A one-token step cannot
+    grow them; it must raise CacheCapacityError and leave every pool byte,
+    reference count, table, length and the free stack as they were, both run
+    eagerly (fused append + attention) and replayed from captured graphs.
+    A blocked row once kept its old length L as the batch length, and the
+    single-token append (positioned at length - 1) overwrote token L - 1 of
+    a valid, shared page in every layer."""
+    from pkv.cache_errors import CacheCapacityError
+    from pkv.device_arena import DevicePageArena, DeviceRunner
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.ops import PageFormat
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16")
+    model = AttentionStack(spec, device="cuda", seed=6)
+    fmt = PageFormat(2, 64, 16, 8, 32, torch.float16)
+    arena = DevicePageArena(fmt, 5, num_layers=2, max_slots=4, max_tokens=256)
+    runner = DeviceRunner(model, arena)
+    a, c, d = arena.open_slot(), arena.open_slot(), arena.open_slot()
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    x0 = torch.randn((3, 32, 256), generator=gen, device="cuda").half()
+    runner.execute([a, c, d], x0, [32, 16, 20])    # pages: a 2, c 1, d 2 -> 5 of 5
+    b = arena.open_slot()
+    arena.fork([a], [b])                           # b shares a's two full pages
+    assert arena.check() == 0
+    slots = [a, b, c, d]                           # a, b, c need a page; d's tail has room
+
+    def snapshot():
+        torch.cuda.synchronize()
+        return ([p.clone() for p in arena.pools], arena.refcounts(), arena.free_stack(),
+                arena.table.clone(), arena.lens.clone())
+
+    def assert_unchanged(before, what):
+        after = snapshot()
+        for l, (p0, p1) in enumerate(zip(before[0], after[0])):
+            assert torch.equal(p0, p1), f"{what}: layer {l}'s pool changed"
+        for name, x0_, x1_ in zip(("refcounts", "free stack", "table", "lengths"),
+                                  before[1:], after[1:]):
+            assert torch.equal(x0_, x1_), f"{what}: {name} changed"
+
+    before = snapshot()
+    mirror = list(arena.lengths)
+    x1 = torch.randn((4, 1, 256), generator=gen, device="cuda").half()
+    with pytest.raises(CacheCapacityError):
+        runner.execute(slots, x1)
+    assert arena.lengths == mirror
+    assert_unchanged(before, "eager step")
+
+    step = runner.capture_decode(slots, x1.clone(), warm=False)
+    for i in range(2):
+        step.replay()
+        with pytest.raises(CacheCapacityError):
+            arena.check()
+        assert_unchanged(before, f"replay {i}")
+    arena.sync_lengths()
+    assert arena.lengths == mirror
+    _invariants(arena)
+
+
 def test_random_operations_keep_the_invariants():
     rng = np.random.default_rng(7)
     arena = _arena(96, max_slots=12, max_tokens=320)
