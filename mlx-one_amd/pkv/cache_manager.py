@@ -113,6 +113,7 @@ class CacheManager:
         self.bundle, self.config = bundle, config
         self.device = device
         self.device_arenas = {}    # (dtype, bits) -> (DevicePageArena, DevicePrefixIndex)
+        self._device_bytes = 0     # page-pool bytes of every device arena, against the budget
         self.block_pool = SegmentedPageArena(config.memory_budget_bytes,
                                              block_tokens=config.block_size_tokens, device=device)
         self.block_prefix = BlockPrefixIndex(config.prefix_cache_budget_bytes,
@@ -178,10 +179,19 @@ class CacheManager:
             fmt = PageFormat(s0.num_kv_heads, s0.key_head_dim, self.config.block_size_tokens,
                              bits or 16, self.config.group_size if bits else 32,
                              getattr(torch, dtype))
+            # Every precision's arena is charged against the one byte budget
+            # (the reference's arena enforces one capacity across all its
+            # segments, engine/arena.py:71): pools are allocated whole, so an
+            # arena takes device_pages pages if set, else what the arenas
+            # opened before it left of the budget.
             per_page = fmt.page_bytes * len(specs)
-            capacity = self.config.device_pages or self.config.memory_budget_bytes // per_page
-            if capacity < 1:
-                raise CacheCapacityError("cache budget below one page per layer", retryable=False)
+            left = self.config.memory_budget_bytes - self._device_bytes
+            capacity = self.config.device_pages or left // per_page
+            if capacity < 1 or capacity * per_page > left:
+                raise CacheCapacityError(
+                    f"device arena for {dtype}/{bits or 16}-bit pages needs "
+                    f"{max(capacity, 1) * per_page} bytes; {max(left, 0)} of the cache budget "
+                    "are left", retryable=False)
             arena = DevicePageArena(fmt, capacity, num_layers=len(specs),
                                     max_slots=self.config.max_sequences +
                                     self.config.prefix_max_entries,
@@ -191,6 +201,7 @@ class CacheManager:
                 self.config.prefix_cache_budget_bytes // per_page, 0),
                 max_entries=self.config.prefix_max_entries)
             self.device_arenas[key] = (arena, prefix)
+            self._device_bytes += capacity * per_page
         return self.device_arenas[key]
 
     def _slot_entries(self, dtype, bits):

@@ -123,6 +123,40 @@ def test_device_manager_failed_and_out_of_page_steps_change_nothing():
     assert out.committed_token_counts == (1, 1) and [h.token_count for h in hs] == [41, 41]
 
 
+def test_device_arenas_of_several_precisions_share_one_budget():
+    """Each precision's device arena is charged against the one byte budget:
+    sized from the budget, the first arena takes all of it and a second
+    precision is refused; with pages per arena given, arenas open while they
+    fit and the bytes allocated never pass the budget."""
+    from pkv.cache_errors import CacheCapacityError
+    from pkv.ops import PageFormat
+
+    # two layers of int8 pages: 100 of them and 64 bytes, which fit no page
+    per_page = 2 * PageFormat(2, 64, 16, 8, 32, torch.float16).page_bytes
+    budget = 100 * per_page + 64
+    _, cm = _setup("device", budget=budget)
+    cm.create_handle("a", key_type="q8_0", value_type="q8_0")
+    assert [dev.capacity for dev, _ in cm.device_arenas.values()] == [100]
+    with pytest.raises(CacheCapacityError):
+        cm.create_handle("b", key_type="q4_0", value_type="q4_0")
+    assert cm.stats().allocated_bytes == 100 * per_page
+    assert cm.stats().live_handles == 1
+
+    budget = 1 << 20
+    _, cm = _setup("device", budget=budget, pages=40)
+    cm.create_handle("a", key_type="q8_0", value_type="q8_0")
+    cm.create_handle("b", key_type="q4_0", value_type="q4_0")
+    cm.create_handle("c", key_type="q8_0", value_type="q8_0")   # same arena: no new bytes
+    pools = [(dev.capacity, len(dev.pools), dev.fmt.page_bytes)
+             for dev, _ in cm.device_arenas.values()]
+    assert [c for c, _, _ in pools] == [40, 40]
+    allocated = sum(c * n * b for c, n, b in pools)
+    assert cm.stats().allocated_bytes == allocated <= budget
+    with pytest.raises(CacheCapacityError):                     # 40 f16 pages do not fit
+        cm.create_handle("d", key_type="f16", value_type="f16")
+    assert cm.stats().allocated_bytes == allocated and len(cm.device_arenas) == 2
+
+
 def test_device_manager_prefix_adoption_gives_the_steps_of_a_recomputed_prompt():
     from pkv.runner import PagedRunner
 
