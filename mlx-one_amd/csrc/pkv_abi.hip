@@ -448,7 +448,15 @@ int pkv_paged_attention_noalloc(void *stream, const pkv_layout *layout, const vo
   if (waves > 0) {
     pkv_geometry geo;
     if (int rc = geometry(layout, &geo)) return rc;
-    const int64_t need = pkv_attention_workspace_bytes(layout, num_heads, num_queries, waves);
+    // Only the split-K decode parts take scratch: a wide call without
+    // per-sequence widths runs the prefill kernel alone and needs none.
+    const bool shaped = num_heads >= 1 && num_queries >= 1 && num_heads % geo.hk == 0 &&
+                        (int64_t)num_queries * (num_heads / geo.hk) <= kMaxRows;
+    const bool prefill_only =
+        shaped && !widths &&
+        !pkv::decode_serves(pkv::to_geo(geo), num_queries * (num_heads / geo.hk));
+    const int64_t need =
+        prefill_only ? 0 : pkv_attention_workspace_bytes(layout, num_heads, num_queries, waves);
     if (need > kNoAllocScratchBytes)
       return fail(PKV_OUT_OF_MEMORY,
                   "pkv_paged_attention_noalloc: " + std::to_string(waves) + " waves need " +

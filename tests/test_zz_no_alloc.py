@@ -104,3 +104,30 @@ def test_noalloc_default_waves_and_refused_sizes():
     code, again = _call(True, w, fmt, pool, table, lengths, q, q_pos, 0)   # still usable
     torch.cuda.synchronize()
     assert code == 0 and torch.equal(again, out)
+
+
+def test_noalloc_plain_prefill_needs_no_scratch_at_any_wave_count():
+    """A wide call without per-sequence widths runs the prefill kernel alone,
+    which takes no split-K scratch: an explicit wave count whose decode
+    partials would pass the fixed array is not refused, and the output equals
+    the workspace entry point's (given a 256-byte workspace it never uses)."""
+    from pkv import _native as nat
+
+    w, inst, fmt, pool, table, lengths, q, q_pos = _case("c5", batch=2, lengths=(300, 90),
+                                                         num_queries=48, append_tokens=48)
+    waves = 100000                     # decode partials for these rows: ~3 GB
+    lib = nat.load()
+    stream = nat.stream_handle(q.device)
+    scale = 1.0 / math.sqrt(w.head_dim)
+    common = (stream, ctypes.byref(fmt.c_layout), nat.ptr(pool), pool.shape[0], nat.ptr(q),
+              w.batch, w.heads, w.num_queries, nat.ptr(table), table.shape[1], nat.ptr(lengths),
+              nat.ptr(q_pos), None, scale, waves)
+    a, b = torch.empty_like(q), torch.empty_like(q)
+    assert lib.pkv_paged_attention_noalloc(*common, nat.ptr(a)) == 0, nat.last_error()
+    ws = torch.empty(256, dtype=torch.uint8, device=q.device)
+    assert lib.pkv_paged_attention(*common, nat.ptr(ws), ws.numel(), nat.ptr(b)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, w.num_queries, np.int32),
+                            scale)
+    assert_attention_close(a.float().cpu().numpy(), want)
