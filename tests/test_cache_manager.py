@@ -211,6 +211,114 @@ def test_prefix_index_evicts_leaves_under_its_budget():
     assert cm.block_pool.nbytes == 0                     # unpinned pages were freed
 
 
+def _pins(cm):
+    return {int(b): blk.pins for b, blk in cm.block_pool._blocks.items() if blk.pins}
+
+
+def test_prefix_index_keeps_recently_looked_up_prompts_and_drops_stale_leaves():
+    """Two prompts of three pages share their first page; after a lookup of
+    the first, a third prompt's publication over budget drops the second
+    prompt's pages (least recently used leaves first), never a page some
+    kept page extends."""
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    index = cm.block_prefix
+    a = tuple(range(49))
+    b = a[:16] + tuple(range(500, 533))
+    c = tuple(range(900, 949))
+    ha, hb, hc = _prefilled(cm, "a", a), _prefilled(cm, "b", b), _prefilled(cm, "c", c)
+    assert index.publish(fp, a, tuple(x.full_block_refs for x in ha.bundle.entries)) == 3
+    # b's first page is a's (same tokens): only its last two are new nodes
+    assert index.publish(fp, b, tuple(x.full_block_refs for x in hb.bundle.entries)) == 2
+    assert index.stats()["entries"] == 5
+    page_set = index.stats()["bytes"] // 5
+    assert index.lookup(fp, a) is not None                   # a is now the most recent
+    index.capacity_bytes = 6 * page_set
+    assert index.publish(fp, c, tuple(x.full_block_refs for x in hc.bundle.entries)) == 3
+    stats = index.stats()
+    assert stats["entries"] == 6 and stats["evictions"] == 2
+    assert index.longest_prefix_tokens(fp, a) == 48
+    assert index.longest_prefix_tokens(fp, b) == 16          # only the shared first page
+    assert index.longest_prefix_tokens(fp, c) == 48
+    # every node pins one page per layer; b's own pages are unpinned again
+    assert sum(_pins(cm).values()) == 6 * 3
+    for cache in hb.bundle.entries:
+        assert all(r.block.pins == 0 for r in cache._blocks)
+
+
+def test_prefix_index_metadata_budget_and_stale_heap_items():
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    index = cm.block_prefix
+    prompt = tuple(range(81))                                 # five complete pages
+    h = _prefilled(cm, "a", prompt)
+    assert index.publish(fp, prompt, tuple(x.full_block_refs for x in h.bundle.entries)) == 5
+    per_node = index.stats()["metadata_bytes"] // 5
+    for _ in range(500):                                      # each lookup re-stamps the path
+        assert index.lookup(fp, prompt).token_count == 80
+    assert len(index._leaves) <= 4 * 5 + 64
+    index.metadata_capacity_bytes = 3 * per_node
+    index.publish(fp, prompt, tuple(x.full_block_refs for x in h.bundle.entries))
+    assert index.stats()["entries"] == 3 and index.longest_prefix_tokens(fp, prompt) == 48
+    assert index.stats()["metadata_bytes"] == 3 * per_node
+
+
+def test_prefix_publication_that_fails_to_pin_leaves_the_index_as_it_was(monkeypatch):
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    index = cm.block_prefix
+    first = tuple(range(33))
+    h = _prefilled(cm, "a", first)
+    index.publish(fp, first, tuple(x.full_block_refs for x in h.bundle.entries))
+    before, pins = index.stats(), _pins(cm)
+    longer = tuple(range(81))
+    h2 = _prefilled(cm, "b", longer)
+    original, calls = cm.block_pool.pin, [0]
+
+    def pin(block_id):
+        calls[0] += 1
+        if calls[0] == 5:                                     # the second new node, 2nd layer
+            raise MemoryError("injected pin failure")
+        return original(block_id)
+
+    monkeypatch.setattr(cm.block_pool, "pin", pin)
+    with pytest.raises(MemoryError):
+        index.publish(fp, longer, tuple(x.full_block_refs for x in h2.bundle.entries))
+    assert index.stats() == before and _pins(cm) == pins
+    assert index.longest_prefix_tokens(fp, longer) == 32
+    monkeypatch.setattr(cm.block_pool, "pin", original)
+    assert index.publish(fp, longer, tuple(x.full_block_refs for x in h2.bundle.entries)) == 3
+    assert index.longest_prefix_tokens(fp, longer) == 80
+    index.clear()
+    assert _pins(cm) == {} and index.stats()["entries"] == 0 and index.nbytes == 0
+
+
+def test_prefix_keys_chain_from_the_fingerprint_digest():
+    """A node's key is the reference's chained key: sha256 over the parent's
+    key and the page's tokens, starting from the fingerprint digest."""
+    import hashlib
+    import json
+
+    from pkv.prefix_cache import chain_key
+
+    cm = _manager(prefix_cache_enabled=True, block_size_tokens=16)
+    fp = cm.fingerprint(key_type="q8_0", value_type="q8_0")
+    prompt = tuple(range(40))
+    h = _prefilled(cm, "a", prompt)
+    cm.block_prefix.publish(fp, prompt, tuple(x.full_block_refs for x in h.bundle.entries))
+    keys, node = [], cm.block_prefix._roots[fp]
+    while node.children:
+        (node,) = node.children.values()
+        keys.append(node.key)
+    parent, want = fp.digest, []
+    for i in range(2):
+        body = json.dumps(list(prompt[16 * i:16 * i + 16]), separators=(",", ":"))
+        parent = hashlib.sha256(parent.encode() + b":" + body.encode()).hexdigest()
+        want.append(parent)
+    assert keys == want == [chain_key(fp.digest, prompt[:16]),
+                            chain_key(want[0], prompt[16:32])]
+
+
 def test_prefix_reuse_rules():
     from pkv.cache_errors import PrefixReuseUnsupported
 
