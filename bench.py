@@ -327,8 +327,8 @@ def layer_bench(args):
         if hidden is None:
             hidden = [torch.randn((n, spec.hidden), generator=gen, device=device,
                                   dtype=torch.float16) for n in widths]
-        reqs = [ForwardRequest(h.request_id, x, h.bundle.entries, phase=phase, runtime=cm,
-                               handle=h)
+        reqs = [ForwardRequest(None, (), h.bundle.entries, phase=phase, runtime=cm,
+                               handle=h, request_id=h.request_id, hidden=x)
                 for h, n, x in zip(handles, widths, hidden) if n > 0]
         return runner.execute(reqs)
 
@@ -413,8 +413,9 @@ def layer_device_bench(args):
     gen.manual_seed(w.seed)
 
     def requests(rows, hidden, phase):
-        return [ForwardRequest(handles[b].request_id, x, handles[b].bundle.entries, phase=phase,
-                               runtime=cm, handle=handles[b]) for b, x in zip(rows, hidden)]
+        return [ForwardRequest(None, (), handles[b].bundle.entries, phase=phase,
+                               runtime=cm, handle=handles[b], request_id=handles[b].request_id,
+                               hidden=x) for b, x in zip(rows, hidden)]
 
     chunk = 1024
     while True:

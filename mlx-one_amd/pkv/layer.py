@@ -52,6 +52,7 @@ class ModelSpec:
     rope_theta: float = 500000.0
     rope_scaling: dict | None = field(default=None)
     dtype: str = "bfloat16"
+    vocab_size: int = 128256
 
     @property
     def layers(self):
@@ -155,9 +156,27 @@ class AttentionStack:
 
     def __init__(self, spec: ModelSpec = ModelSpec(), *, device="cuda", seed=0):
         self.spec = spec
+        self.device, self.seed = device, seed
         self.layers = tuple(AttentionLayer(spec, i, device=device, seed=seed)
                             for i in range(spec.num_layers))
         self.activation_dtype = spec.dtype
+        self._embedding = None
+
+    def embed(self, token_ids):
+        """``[T, hidden]`` inputs of the first layer for token ids: rows of a
+        random (seeded) embedding table, built on first use."""
+        import torch
+
+        ids = torch.as_tensor(list(token_ids), dtype=torch.int64)
+        if ids.numel() < 1 or int(ids.min()) < 0 or int(ids.max()) >= self.spec.vocab_size:
+            raise ValueError(f"token ids must lie in [0, {self.spec.vocab_size})")
+        if self._embedding is None:
+            gen = torch.Generator(device=self.device)
+            gen.manual_seed(1000 * self.seed + 999)
+            table = torch.randn((self.spec.vocab_size, self.spec.hidden), generator=gen,
+                                device=self.device)
+            self._embedding = table.to(getattr(torch, self.spec.dtype))
+        return self._embedding[ids.to(self._embedding.device)]
 
     def forward(self, x, *, cache, position_ids):
         for layer, layer_cache in zip(self.layers, cache, strict=True):

@@ -96,27 +96,29 @@ def test_runner_rejects_inconsistent_batches():
     runner = PagedRunner(_Model(cm.bundle.spec))
     h1 = cm.create_handle("a", key_type="bf16", value_type="bf16")
     h2 = cm.create_handle("b", key_type="bf16", value_type="bf16")
-    ok = ForwardRequest("a", _Hidden(1, 256), h1.bundle.entries, runtime=cm, handle=h1)
+    ok = ForwardRequest(None, (), h1.bundle.entries, runtime=cm, handle=h1, request_id="a",
+                        hidden=_Hidden(1, 256))
     with pytest.raises(ValueError):
         runner.execute([])
     with pytest.raises(ValueError):        # another phase in the batch
-        runner._validate([ok, ForwardRequest("b", _Hidden(1, 256), h2.bundle.entries,
-                                             phase="prefill", runtime=cm, handle=h2)])
+        runner._validate(runner.model, [ok, ForwardRequest(None, (), h2.bundle.entries,
+                                             phase="prefill", runtime=cm, handle=h2, request_id="b",
+                                             hidden=_Hidden(1, 256))])
     with pytest.raises(ValueError):        # layers out of order
-        runner._validate([ForwardRequest("a", _Hidden(1, 256), h1.bundle.entries[::-1],
-                                         runtime=cm)])
+        runner._validate(runner.model, [ForwardRequest(None, (), h1.bundle.entries[::-1],
+                                         runtime=cm, request_id="a", hidden=_Hidden(1, 256))])
     with pytest.raises(ValueError):        # the request does not own its caches
-        runner._validate([ForwardRequest("a", _Hidden(1, 256), h2.bundle.entries, runtime=cm,
-                                         handle=h1)])
+        runner._validate(runner.model, [ForwardRequest(None, (), h2.bundle.entries, runtime=cm,
+                                         handle=h1, request_id="a", hidden=_Hidden(1, 256))])
     with pytest.raises(ValueError):        # hidden size of another model
-        runner._validate([ForwardRequest("a", _Hidden(1, 128), h1.bundle.entries, runtime=cm,
-                                         handle=h1)])
+        runner._validate(runner.model, [ForwardRequest(None, (), h1.bundle.entries, runtime=cm,
+                                         handle=h1, request_id="a", hidden=_Hidden(1, 128))])
     hq = cm.create_handle("q", key_type="q8_0", value_type="q8_0")   # f16 pages, bf16 model
     from pkv.modes import ModelCapabilityUnsupported
     with pytest.raises(ModelCapabilityUnsupported):
-        runner._validate([ForwardRequest("q", _Hidden(1, 256), hq.bundle.entries, runtime=cm,
-                                         handle=hq)])
-    runner._validate([ok])
+        runner._validate(runner.model, [ForwardRequest(None, (), hq.bundle.entries, runtime=cm,
+                                         handle=hq, request_id="q", hidden=_Hidden(1, 256))])
+    runner._validate(runner.model, [ok])
     with pytest.raises(ValueError):
         RunnerOutput(("a", "a"), (None, None), (1, 1))
 

@@ -364,8 +364,9 @@ def test_device_runner_matches_the_host_runner_and_rolls_back():
             x[b, n:] = 0
         got = dev.execute(slots, x, widths)
         phase = "prefill" if width > 1 else "decode"
-        out = host.execute([ForwardRequest(h.request_id, x[b, :n], h.bundle.entries, phase=phase,
-                                           runtime=cm, handle=h, return_all_logits=True)
+        out = host.execute([ForwardRequest(None, (), h.bundle.entries, phase=phase,
+                                           runtime=cm, handle=h, return_all_logits=True,
+                                           request_id=h.request_id, hidden=x[b, :n])
                             for b, (h, n) in enumerate(zip(handles, widths))])
         torch.cuda.synchronize()
         for b, n in enumerate(widths):
@@ -393,7 +394,8 @@ def test_device_runner_matches_the_host_runner_and_rolls_back():
     x = torch.randn((3, 1, 256), generator=gen, device="cuda").half()
     step = dev.capture_decode(slots, x)                # one eager step, then the graph
     out = step.out
-    host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm, handle=h)
+    host.execute([ForwardRequest(None, (), h.bundle.entries, runtime=cm, handle=h,
+                                 request_id=h.request_id, hidden=x[b])
                   for b, h in enumerate(handles)])     # the host runner takes the same step
     # the graph's split-K partials live in a workspace the step holds: dropping
     # and refilling the shared per-device workspace must not reach the replays
@@ -409,8 +411,9 @@ def test_device_runner_matches_the_host_runner_and_rolls_back():
             junk.append(torch.full((8 << 20,), -1.0, device="cuda"))
         x.copy_(torch.randn((3, 1, 256), generator=gen, device="cuda").half())
         step.replay()
-        ref = host.execute([ForwardRequest(h.request_id, x[b], h.bundle.entries, runtime=cm,
-                                           handle=h) for b, h in enumerate(handles)])
+        ref = host.execute([ForwardRequest(None, (), h.bundle.entries, runtime=cm,
+                                           handle=h, request_id=h.request_id,
+                                           hidden=x[b]) for b, h in enumerate(handles)])
         torch.cuda.synchronize()
         for b in range(3):
             assert torch.equal(out[b, 0], ref.logits[b][0, 0]), (i, b)

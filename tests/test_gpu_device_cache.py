@@ -43,8 +43,9 @@ def _setup(page_arena, *, budget=1 << 28, prefix=False, key_type="q8_0", seed=5,
 def _run(runner, cm, handles, xs, phase="prefill"):
     from pkv.runner import ForwardRequest
 
-    return runner.execute([ForwardRequest(h.request_id, x, h.bundle.entries, phase=phase,
-                                          runtime=cm, handle=h, return_all_logits=True)
+    return runner.execute([ForwardRequest(None, (), h.bundle.entries, phase=phase,
+                                          runtime=cm, handle=h, return_all_logits=True,
+                                          request_id=h.request_id, hidden=x)
                            for h, x in zip(handles, xs)])
 
 

@@ -131,9 +131,10 @@ def test_runner_prefill_then_decode_matches_reference(case, copy_on_write):
     widths_seq = [prefill] + [(1,) * len(prefill)] * steps
     for step, widths in enumerate(widths_seq):
         hidden = [rng.standard_normal((w, spec.hidden)).astype(np.float32) for w in widths]
-        reqs = [ForwardRequest(h.request_id, torch.from_numpy(x).to("cuda", dtype),
-                               h.bundle.entries, phase="prefill" if step == 0 else "decode",
-                               runtime=cm, handle=h, return_all_logits=step == 0)
+        reqs = [ForwardRequest(None, (), h.bundle.entries, phase="prefill" if step == 0 else "decode",
+                               runtime=cm, handle=h, return_all_logits=step == 0,
+                               request_id=h.request_id,
+                               hidden=torch.from_numpy(x).to("cuda", dtype))
                 for h, x in zip(handles, hidden)]
         out = runner.execute(reqs)
         want = ref.step(hidden)
@@ -181,8 +182,9 @@ def test_failed_step_leaves_caches_unchanged(copy_on_write):
 
     def requests(widths, phase):
         hidden = [rng.standard_normal((w, spec.hidden)).astype(np.float32) for w in widths]
-        return hidden, [ForwardRequest(h.request_id, torch.from_numpy(x).to("cuda", torch.float16),
-                                       h.bundle.entries, phase=phase, runtime=cm, handle=h)
+        return hidden, [ForwardRequest(None, (), h.bundle.entries, phase=phase, runtime=cm,
+                                       handle=h, request_id=h.request_id,
+                                       hidden=torch.from_numpy(x).to("cuda", torch.float16))
                         for h, x in zip(handles, hidden)]
 
     hidden, reqs = requests((15, 16), "prefill")   # a partial page and a page just filled
@@ -224,8 +226,9 @@ def test_adopted_prefix_pages_give_the_same_steps_as_computed_ones():
     hidden = torch.randn((53, 256), generator=gen, device="cuda").half()
 
     def run(handle, x, phase):
-        return runner.execute([ForwardRequest(handle.request_id, x, handle.bundle.entries,
-                                              phase=phase, runtime=cm, handle=handle)])
+        return runner.execute([ForwardRequest(None, (), handle.bundle.entries,
+                                              phase=phase, runtime=cm, handle=handle,
+                                              request_id=handle.request_id, hidden=x)])
 
     a = cm.create_handle("a", key_type="q8_0", value_type="q8_0")
     c = cm.create_handle("c", key_type="q8_0", value_type="q8_0")
@@ -266,8 +269,9 @@ def test_snapshot_restore_gives_the_same_steps(tmp_path):
     runner = PagedRunner(model)
     gen = torch.Generator(device="cuda").manual_seed(6)
     a = cm.create_handle("a", key_type="q4_0", value_type="q4_0")
-    runner.execute([ForwardRequest("a", torch.randn((45, 256), generator=gen, device="cuda").half(),
-                                   a.bundle.entries, phase="prefill", runtime=cm, handle=a)])
+    runner.execute([ForwardRequest(None, (), a.bundle.entries, phase="prefill", runtime=cm,
+                                   handle=a, request_id="a",
+                                   hidden=torch.randn((45, 256), generator=gen, device="cuda").half())])
     manifest = save_snapshot(tmp_path, a.bundle, identity="m", reference_pages=True)
     restored = load_snapshot(tmp_path, identity="m", expected_specs=cm2.layer_specs,
                              page_pool=cm2.block_pool, bits=4)
@@ -287,8 +291,10 @@ def test_snapshot_restore_gives_the_same_steps(tmp_path):
         assert np.array_equal(data[f"layer_0_reference_{name}"], value.cpu().numpy()), name
     for _ in range(3):
         x = torch.randn((1, 256), generator=gen, device="cuda").half()
-        out_a = runner.execute([ForwardRequest("a", x, a.bundle.entries, runtime=cm, handle=a)])
-        out_b = runner.execute([ForwardRequest("b", x, b.bundle.entries, runtime=cm2, handle=b)])
+        out_a = runner.execute([ForwardRequest(None, (), a.bundle.entries, runtime=cm, handle=a,
+                                               request_id="a", hidden=x)])
+        out_b = runner.execute([ForwardRequest(None, (), b.bundle.entries, runtime=cm2, handle=b,
+                                               request_id="b", hidden=x)])
         torch.cuda.synchronize()
         assert torch.equal(out_a.logits[0], out_b.logits[0])
 
@@ -318,13 +324,14 @@ def test_every_page_allocation_of_a_step_rolls_back(copy_on_write, monkeypatch):
     def fresh():
         cm = CacheManager(model, config)
         h = cm.create_handle("r", key_type="q8_0", value_type="q8_0")
-        runner.execute([ForwardRequest("r", first, h.bundle.entries, phase="prefill",
-                                       runtime=cm, handle=h)])
+        runner.execute([ForwardRequest(None, (), h.bundle.entries, phase="prefill",
+                                       runtime=cm, handle=h, request_id="r", hidden=first)])
         return cm, h
 
     def run(cm, h, x):
-        return runner.execute([ForwardRequest("r", x, h.bundle.entries, phase="prefill",
-                                              runtime=cm, handle=h, return_all_logits=True)])
+        return runner.execute([ForwardRequest(None, (), h.bundle.entries, phase="prefill",
+                                              runtime=cm, handle=h, return_all_logits=True,
+                                              request_id="r", hidden=x)])
 
     # the untouched twin, and the number of allocations the step makes
     cm0, h0 = fresh()
@@ -404,3 +411,96 @@ def test_device_runner_out_of_pages_at_every_point_changes_nothing():
         assert arena.lengths == mirror
         assert torch.equal(arena.lens, lens) and torch.equal(arena.table, table)
         assert torch.equal(arena.refcounts(), refs) and torch.equal(arena.free_stack(), stack)
+
+
+@pytest.mark.parametrize("page_arena", ["host", "device"])
+def test_reference_style_requests_trace_and_cancellation(page_arena):
+    """The reference's runner tests with the real kernels, on both arenas:
+    requests built positionally from token ids (the model embeds them) run
+    under ``PagedRunner()``, which takes the model from the bundle, and give
+    the outputs of the same steps fed as hidden states, bit for bit; the trace
+    carries the reference's keys (``tests/test_paged_hybrid.py:162-163``,
+    ``tests/test_p1_runtime.py:517``); a request cancelled while its forward
+    runs keeps its caches (``tests/test_paged_hybrid.py:183-186``), so its next
+    step gives what it gives in a run where the cancelled step never happened."""
+    import threading
+
+    from pkv.cache_manager import CacheConfig, CacheManager
+    from pkv.layer import AttentionStack, ModelSpec
+    from pkv.runner import ForwardRequest, PagedRunner
+
+    spec = ModelSpec(hidden=256, query_heads=8, kv_heads=2, head_dim=64, num_layers=2,
+                     dtype="float16", vocab_size=1000)
+    model = AttentionStack(spec, device="cuda", seed=7)
+
+    def manager():
+        return CacheManager(model, CacheConfig(block_size_tokens=16, key_type="q8_0",
+                                               value_type="q8_0", group_size=32,
+                                               memory_budget_bytes=1 << 26, page_arena=page_arena,
+                                               max_sequences=4, max_sequence_tokens=256))
+
+    prompts = [tuple(range(1, 18)), (4, 5, 6)]
+    cm_t, cm_h, cm_c = manager(), manager(), manager()
+    by_tokens, by_hidden, clean = [], [], []
+    for i, ids in enumerate(prompts):
+        for cm, out in ((cm_t, by_tokens), (cm_h, by_hidden), (cm_c, clean)):
+            h = cm.create_handle(str(i), key_type="q8_0", value_type="q8_0")
+            out.append(ForwardRequest(model, ids, h.bundle.entries, "prefill", ids, cm, h,
+                                      request_id=str(i)))
+    for r in by_hidden:
+        r.hidden = model.embed(r.token_ids)
+    runner, runner_h, runner_c = PagedRunner(), PagedRunner(), PagedRunner()
+
+    def step(requests, rn, tokens=None):
+        if tokens is not None:
+            for r in requests:
+                r.phase, r.token_ids = "decode", tokens
+                if r.hidden is not None:
+                    r.hidden = model.embed(tokens)
+        return rn.execute(tuple(requests))
+
+    a, b = step(by_tokens, runner), step(by_hidden, runner_h)
+    step(clean, runner_c)
+    torch.cuda.synchronize()
+    for x, y in zip(a.logits, b.logits):
+        assert torch.equal(x, y)
+    trace = runner.last_trace
+    assert trace["history_materializations"] == 0 and trace["direct_attention_calls"] == 2
+    assert trace["history_lengths"] == [0, 0] and trace["layer_layouts"][1]["key_dim"] == 64
+    for k in range(2):
+        a, b = step(by_tokens, runner, (9 + k,)), step(by_hidden, runner_h, (9 + k,))
+        step(clean, runner_c, (9 + k,))
+        torch.cuda.synchronize()
+        for x, y in zip(a.logits, b.logits):
+            assert torch.equal(x, y), k
+        assert runner.last_trace["history_lengths"] == [17 + k, 3 + k]
+        assert runner.last_trace["history_materializations"] == 0
+    before = [r.cache[0].offset for r in by_tokens]
+    by_tokens[0].cancel = threading.Event()
+    forward = model.forward
+
+    def cancelling(*args, **kwargs):
+        out = forward(*args, **kwargs)
+        by_tokens[0].cancel.set()
+        return out
+
+    model.forward = cancelling
+    try:
+        step(by_tokens, runner, (40,))
+    finally:
+        model.forward = forward
+    assert [r.cache[0].offset for r in by_tokens] == [before[0], before[1] + 1]
+    assert by_tokens[0].handle.token_count == before[0]
+    assert runner.last_trace["cancelled_request_ids"] == ["0"]
+    # the clean run: request 1 takes the step request 0 missed, alone
+    clean[1].phase, clean[1].token_ids = "decode", (40,)
+    runner_c.execute((clean[1],))
+    by_tokens[0].cancel = None
+    a, c = step(by_tokens, runner, (41,)), step(clean, runner_c, (41,))
+    torch.cuda.synchronize()
+    assert [r.cache[0].offset for r in by_tokens] == [r.cache[0].offset for r in clean]
+    # request 0's caches saw the same steps in both runs: the same bits
+    assert torch.equal(a.logits[0], c.logits[0])
+    # request 1 took token 40 in a batch of one in the clean run, where the
+    # projection GEMM may round differently
+    torch.testing.assert_close(a.logits[1], c.logits[1], atol=2e-2, rtol=0)
