@@ -73,6 +73,14 @@ __device__ __forceinline__ void load_meta(uint32_t (&mw)[C::MW], const uint8_t *
 template <int BITS>
 struct Conv;
 
+// bf16 pair of the codes in bytes i0 (low half) and i1 (high half) of w: a
+// code c <= 255 converts to f32 exactly (v_cvt_f32_ubyte), and its upper 16
+// bits are c as bf16, exact since c has at most 8 significant bits.
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t w, int i0, int i1) {
+  const float f0 = (float)((w >> (8 * i0)) & 0xFFu), f1 = (float)((w >> (8 * i1)) & 0xFFu);
+  return perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
 template <>
 struct Conv<8> {
   template <int LW>
@@ -87,6 +95,12 @@ struct Conv<8> {
     const uint32_t w0 = w[n];
     u2 r = {perm(w0, kMagic, kSelLo), perm(w0, kMagic, kSelHi)};
     return __builtin_bit_cast(h4, r);
+  }
+  // The codes of kop (same element order) as bf16 values c.
+  template <int LW>
+  static __device__ __forceinline__ u4 kop_bf16(const uint32_t (&w)[LW], int kb) {
+    const uint32_t w0 = w[2 * kb], w1 = w[2 * kb + 1];
+    return u4{bf16_pair(w0, 0, 1), bf16_pair(w0, 2, 3), bf16_pair(w1, 0, 1), bf16_pair(w1, 2, 3)};
   }
 };
 
@@ -115,6 +129,14 @@ struct Conv<4> {
     const uint32_t nb = (n & 1) ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
     u2 r = {perm(nb, kMagic, kNibLo), perm(nb, kMagic, kNibHi)};
     return __builtin_bit_cast(h4, r);
+  }
+  // The codes of kop (same element order: nibbles 0, 4, 1, 5, 2, 6, 3, 7)
+  // as bf16 values c.
+  template <int LW>
+  static __device__ __forceinline__ u4 kop_bf16(const uint32_t (&w)[LW], int kb) {
+    const uint32_t x = w[kb];
+    const uint32_t ev = x & 0x0F0F0F0Fu, od = (x >> 4) & 0x0F0F0F0Fu;
+    return u4{bf16_pair(ev, 0, 2), bf16_pair(od, 0, 2), bf16_pair(ev, 1, 3), bf16_pair(od, 1, 3)};
   }
 };
 

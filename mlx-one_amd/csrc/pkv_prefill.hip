@@ -12,12 +12,25 @@
 // query rows); wave w owns 16*RB rows as RB 16-column MFMA row tiles.  The
 // span is streamed in stages of 8 tiles (128 tokens).  Per stage each wave
 // loads ONE tile of quantized K/V (plus its scale/bias words) from HBM into
-// registers a stage ahead, dequantizes it once (packed f16: (1024+c) - 1024,
-// then c*scale + bias) and writes the f16 image into the LDS stage buffer
-// that all eight waves read: K as [tile][token][dim], V transposed as
-// [dim][token slot].  Dequantization thus costs 1/8 of the span per wave, a
-// stage's four steps give the next stage's loads time to land, and the inner
-// loop is a plain f16 flash-attention step:
+// registers a stage ahead, converts it once and writes it into the LDS stage
+// image that all eight waves read: K as [tile][token][dim], V transposed as
+// [dim][token slot].  Conversion thus costs 1/8 of the span per wave, and a
+// stage's four steps give the next stage's loads time to land.
+//
+// Scores keep the reference's float32 precision (engine/paged_attention.py:
+// 82-83: the query dotted with keys dequantized in f32).  The K image holds
+// the codes themselves (exact f16 integers) and the scores are assembled from
+// per-group products on the MFMA pipe:
+//   s = sum_g scale_g * (q_g . c_g) + sum_g bias_g * (sum of q_g)
+// The group chains share one accumulator: after group g's MFMAs it is
+// multiplied by scale_g / scale_{g+1} (f32, per token), so it ends as
+// (sum_g scale_g * q_g.c_g) / scale_last; one FMA by scale_last*scale*log2(e)
+// less the running max gives the exp2 argument, and one 16x16x16 MFMA adds
+// the bias term (the f16 biases times the rows' f32 group sums, split into
+// f16 parts that carry 33 bits) through its accumulator input.  V is
+// dequantized into the image in packed f16 ((1024+c) - 1024, then
+// c*scale + bias: one rounding, relative 2^-11, entering the output
+// linearly).  The inner loop per step:
 //   S^T = K.Q^T        v_mfma_f32_16x16x32_f16, two tiles per step
 //   online softmax     per column, exp2 domain, lazy rescale
 //   O^T += V^T.P^T     v_mfma_f32_16x16x32_f16 over the step's 32 tokens
@@ -60,6 +73,15 @@ struct StageImage {
   static constexpr int K_ELEMS = TILES * KTILE;
   static constexpr int ELEMS = K_ELEMS + DP * VROW;
 };
+
+// Score metadata of quantized K tiles (next to the stage image), per tile:
+//   mult [NG][16 tokens] f32: scale_g / scale_{g+1} for g < NG - 1, then
+//        scale_last * softmax scale * log2(e); 0 for absent tokens
+//   bias [16 tokens][16 slots] f16: the A operand of the bias MFMA, slot k
+//        holding bias_{k / SPG} (SPG slots per group, one per part of the
+//        query's group sum), 0 past the groups and for absent tokens
+// SPG: 3 parts (33 significant bits) while 3 * NG <= 16, else 2 (22 bits).
+constexpr int bias_parts(int ng) { return 3 * ng <= 16 ? 3 : 2; }
 
 // Workgroup barrier once this wave's LDS operations have completed.  No
 // memory fence: __syncthreads() would also wait for the next stage's HBM
@@ -155,15 +177,30 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   constexpr int ROWS = prefill_rows(DP);
   using C = Cfg<BITS, DP, G, RB, FK, 1>;
   constexpr bool QUANT = C::QUANT;
-  constexpr bool F16 = QUANT || FK == 1;  // f16 operands, else bf16
+  // Operand types.  S = K.Q^T takes the query in its own dtype (FK: bf16 0,
+  // f16 1), so the query operand is the query exactly, and K in the same
+  // type (codes are exact in either).  O += V.P^T runs in f16 for quantized
+  // pages (V dequantized into the image) and in the page dtype otherwise.
+  constexpr bool QF16 = FK == 1;
+  constexpr bool PF16 = QUANT || FK == 1;
   constexpr int NG = C::NG, KB = C::KB, NB = C::NB, LW = C::LW;
   using I = StageImage<DP>;
-  typedef typename std::conditional<F16, h8, b8>::type OT;  // 8-element MFMA operand
+  typedef typename std::conditional<QF16, h8, b8>::type QT;  // 8-element QK operand
+  typedef typename std::conditional<PF16, h8, b8>::type PT;  // 8-element PV operand
+  // The bias MFMA in bf16 (range of any query, no scaled rows) when its slots
+  // fit one 16x16x16 MFMA: two parts of each bias (exact) times three of each
+  // group sum, 6 per group; else in f16 (exact biases times 3 or 2 parts).
+  constexpr bool BF16_BIAS = QUANT && 6 * NG <= 16;
+  typedef typename std::conditional<BF16_BIAS, s4, h4>::type BT;  // bias MFMA operand
 
   __shared__ __attribute__((aligned(16))) int s_valid[2][kStageTiles];
   __shared__ int s_lim[2][kPrefillWaves];
   __shared__ int64_t s_zero[SHARE ? 2 : 1];  // zero share: first row, end
   __shared__ __attribute__((aligned(16))) uint16_t stage[2][I::ELEMS];
+  // score metadata of the stage's K tiles (quantized pages)
+  constexpr int SPG = BF16_BIAS ? 6 : bias_parts(NG);
+  __shared__ __attribute__((aligned(16))) float s_mult[2][QUANT ? kStageTiles * NG * 16 : 4];
+  __shared__ __attribute__((aligned(16))) uint16_t s_bias[2][QUANT ? kStageTiles * 16 * 16 : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -232,13 +269,10 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 
   // ---- the wave's query rows: row = ROWS*rblk + 16*RB*wv + 16*rb + col
   int lim[RB];
-  OT qv[RB][KB];
-  // The query operand is the query itself (bf16 -> f16 is exact in range);
-  // scale*log2(e) is applied to the f32 scores (rsc), never rounded into the
-  // operand.  f16 operands hold at most 65504: a row whose largest element
-  // reaches 2^15 is scaled by a power of two sc into [2^14, 2^15) (exact),
-  // which its rsc undoes.
-  float sc[RB], rsc[RB];
+  QT qv[RB][KB];
+  // The query operand is the query itself; scale*log2(e) is applied to the
+  // f32 scores, never rounded into the operand.
+  const float rsc = a.scale_log2;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
@@ -249,7 +283,6 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     const int pos = a.q_pos ? a.q_pos[(int64_t)b * a.nq + qi] : L - width + qi;
     lim[rb] = live ? min(pos, L - 1) : -1;
     const uint16_t *qrow = a.q + (((int64_t)b * a.heads + h) * a.nq + qi) * g.dim;
-    float mx = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int d0 = 32 * kb + 8 * jj;
@@ -265,41 +298,89 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (!valid || d0 + e >= g.dim) e8[e] = 0;
-      OT v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = bits_to_float(e8[e], g.float_kind);
-        mx = fmaxf(mx, fabsf(x));
-        if constexpr (F16) v[e] = (_Float16)x;
-        else v[e] = (__bf16)x;
-      }
-      qv[rb][kb] = v;
+      qv[rb][kb] = __builtin_bit_cast(QT, u4{e8[0] | ((uint32_t)e8[1] << 16), e8[2] | ((uint32_t)e8[3] << 16),
+                                             e8[4] | ((uint32_t)e8[5] << 16), e8[6] | ((uint32_t)e8[7] << 16)});
     }
-    sc[rb] = 1.0f;
-    if constexpr (F16) {
-      // the row's largest |q| (lanes jj share the row); a scaled row
-      // converts again from memory (rare: huge queries only)
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      if (mx >= 32768.0f && mx < INFINITY) {
-        int ex;
-        frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-        sc[rb] = ldexpf(1.0f, 15 - ex);
+  }
+
+  // Exact scores (quantized pages): per row block the B operand of the bias
+  // MFMA, the row's group sums of q times scale*log2(e), Q_g, in parts (the
+  // lane holds slots 4jj..4jj+3).  bf16 parts carry any magnitude.  f16
+  // parts (four or more groups) hold |Q_g| < 2^15: a row whose largest |Q_g|
+  // reaches it has its Q_g scaled by 2^-e, the MFMA then adds the bias term
+  // scaled by 2^-e to an accumulator scaled the same way, and the result is
+  // scaled back by 2^e; a wave holding such a row takes that general form of
+  // the final step (`wide`, a uniform branch).
+  BT qop[QUANT ? RB : 1];
+  float dn[QUANT ? RB : 1], ue[QUANT ? RB : 1];
+  bool wide_lane = false;
+  if constexpr (QUANT) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const int d0 = 32 * kb + 8 * jj;
-          OT v;
+    for (int rb = 0; rb < RB; ++rb) {
+      float qs[NG];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint16_t bits = valid && d0 + e < g.dim ? qrow[d0 + e] : 0;
-            v[e] = (_Float16)(bits_to_float(bits, g.float_kind) * sc[rb]);
-          }
-          qv[rb][kb] = v;
+      for (int gi = 0; gi < NG; ++gi) qs[gi] = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        float t = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += (float)qv[rb][kb][e];
+        qs[(32 * kb) / G] += t;
+      }
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        qs[gi] += __shfl_xor(qs[gi], 16, 64);
+        qs[gi] += __shfl_xor(qs[gi], 32, 64);
+        qs[gi] *= rsc;
+      }
+      BT op = {0, 0, 0, 0};
+      auto place = [&](int k, auto v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((k & 3) == i) op[i] = (k >> 2) == jj ? v : op[i];
+      };
+      if constexpr (BF16_BIAS) {
+        dn[rb] = ue[rb] = 1.0f;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          // three bf16 parts (24 bits): hi, mid, lo; each remainder is exact in f32
+          const uint16_t hi = f32_to_bf16_bits(qs[gi]);
+          const float r1 = qs[gi] - __uint_as_float((uint32_t)hi << 16);
+          const uint16_t mid = f32_to_bf16_bits(r1);
+          const uint16_t lo = f32_to_bf16_bits(r1 - __uint_as_float((uint32_t)mid << 16));
+          const short part[3] = {(short)hi, (short)mid, (short)lo};
+#pragma unroll
+          for (int pt = 0; pt < SPG; ++pt) place(gi * SPG + pt, part[pt % 3]);
+        }
+      } else {
+        float qmax = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) qmax = fmaxf(qmax, fabsf(qs[gi]));
+        int e = 0;
+        if (qmax >= 32768.0f && qmax < INFINITY) {
+          int ex;
+          frexpf(qmax, &ex);  // qmax in [2^(ex-1), 2^ex): qmax * 2^(15-ex) < 2^15
+          e = ex - 15;
+        }
+        dn[rb] = ldexpf(1.0f, -e);
+        ue[rb] = ldexpf(1.0f, e);
+        wide_lane |= e != 0;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          const float x = qs[gi] * dn[rb];
+          const _Float16 hi = (_Float16)x;
+          const float r1 = x - (float)hi;
+          const _Float16 mid = (_Float16)r1;
+          const _Float16 lo = (_Float16)(r1 - (float)mid);
+          const _Float16 part[3] = {hi, mid, lo};
+#pragma unroll
+          for (int pt = 0; pt < SPG; ++pt) place(gi * SPG + pt, part[pt]);
         }
       }
+      qop[rb] = op;
     }
-    rsc[rb] = a.scale_log2 / sc[rb];  // sc is a power of two: exact
   }
+  const bool wide = QUANT && !BF16_BIAS && __any(wide_lane);
 
   // ---- the block's visible span: tokens up to the largest limit; tiles
   // below the smallest live limit are seen whole by every live row
@@ -421,14 +502,55 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) vm[e * NG + gi] = whole || vvalid[e] ? rvm[e * NG + gi] : 0u;
+      // K: the codes as exact integers in the query dtype (f16:
+      // (1024 + c) - 1024; bf16: through f32), and the token's score
+      // metadata (lane (col, jj): multiplier rows g = jj, jj + 4, bias slots
+      // 4jj..4jj+3)
 #pragma unroll
       for (int kb = 0; kb < (k_half ? KB : 0); ++kb) {
-        const h2 sb = __builtin_bit_cast(h2, km[(32 * kb) / G]);
-        const h8 sc = {sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x};
-        const h8 bi = {sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y};
-        const h8 c = Conv<BITS>::template kop<LW>(rk, kb);
-        const h8 v = __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi);
-        *(u4 *)(kdst + 32 * kb) = __builtin_bit_cast(u4, v);
+        if constexpr (QF16) {
+          const h8 c = Conv<BITS>::template kop<LW>(rk, kb) - (_Float16)1024.0f;
+          *(u4 *)(kdst + 32 * kb) = __builtin_bit_cast(u4, c);
+        } else {
+          *(u4 *)(kdst + 32 * kb) = Conv<BITS>::template kop_bf16<LW>(rk, kb);
+        }
+      }
+      if (k_half) {
+        const bool tv = whole || kvalid;
+        float scl[NG];
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) scl[gi] = f16_bits_to_f32(km[gi]);
+        float *mrow = s_mult[dst] + wv * NG * 16 + col;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          if ((gi & 3) != jj) continue;
+          const float mv = gi + 1 < NG ? scl[gi] / scl[gi + 1 < NG ? gi + 1 : gi]
+                                       : scl[gi] * a.scale_log2;
+          mrow[gi * 16] = tv ? mv : 0.0f;
+        }
+        // slot k of group g = k / SPG: the f16 bias, or (bf16 bias MFMA) its
+        // first part (bf16 rounding, slots 0-2 of the group) and the exact
+        // remainder (slots 3-5)
+        s4 bo = {0, 0, 0, 0};
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          const uint32_t bb = km[gi] >> 16;
+          short part[2] = {(short)bb, (short)bb};
+          if constexpr (BF16_BIAS) {
+            const float bf = f16_bits_to_f32(bb);
+            const uint16_t hi = f32_to_bf16_bits(bf);
+            part[0] = (short)hi;
+            part[1] = (short)f32_to_bf16_bits(bf - __uint_as_float((uint32_t)hi << 16));
+          }
+#pragma unroll
+          for (int pt = 0; pt < SPG; ++pt) {
+            const int k = gi * SPG + pt;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if ((k & 3) == i) bo[i] = (k >> 2) == jj ? part[BF16_BIAS && pt >= 3] : bo[i];
+          }
+        }
+        *(u2 *)(s_bias[dst] + (wv * 16 + col) * 16 + 4 * jj) = __builtin_bit_cast(u2, bo);
       }
 #pragma unroll
       for (int n = 0; n < (k_half ? 0 : NB); ++n) {
@@ -462,12 +584,19 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     if (!k_half && lane == 0) s_valid[dst][wv] = r_ok;
   };
 
+  // Row sums of P: f16 P operands (quantized and f16 pages) sum on the MFMA
+  // pipe, as the V^T row of a ones operand (row 0 of OS[rb], lanes jj = 0),
+  // the same rounded P the output accumulates; bf16 pages (P = hi + lo) sum
+  // the f32 probabilities on the VALU.
+  constexpr bool MSUM = PF16;
   float m[RB], lsum[RB];
+  f4 OS[MSUM ? RB : 1];
   f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     m[rb] = -INFINITY;
     lsum[rb] = 0.0f;
+    if constexpr (MSUM) OS[rb] = f4{0, 0, 0, 0};
 #pragma unroll
     for (int n = 0; n < NB; ++n) O[rb][n] = f4{0, 0, 0, 0};
   }
@@ -483,7 +612,11 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // ---- one step covers tiles 2pr and 2pr + 1 of a stage image.
   // S^T = K.Q^T for both tiles; the scores then become v = s*rsc - mb in the
   // exp2 domain (mb: the running max, 0 before any token is seen).
-  auto qk = [&](const uint16_t *img, int pr, f4 (&S)[2][RB], float (&mb)[RB]) __attribute__((always_inline)) {
+  // Quantized pages: the group chains share the accumulator (scaled by
+  // scale_g / scale_{g+1} between groups), then the exp2 argument less the
+  // bias term, then the bias MFMA; S ends as the exp2 argument itself.
+  auto qk = [&](const uint16_t *img, const float *mult, const uint16_t *bias, int pr,
+                f4 (&S)[2][RB], float (&mb)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       mb[rb] = m[rb] == -INFINITY ? 0.0f : m[rb];
@@ -493,15 +626,53 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     const uint16_t *kbase = img + 2 * pr * I::KTILE + col * I::KROW + 8 * jj;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      if constexpr (QUANT) {
+        if (kb > 0 && (32 * kb) % G == 0) {  // group boundary: scale_g / scale_{g+1}
+          const int gprev = (32 * kb) / G - 1;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const f4 r = *(const f4 *)(mult + ((2 * pr + i) * NG + gprev) * 16 + 4 * jj);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) S[i][rb] *= r;
+          }
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const OT kop = __builtin_bit_cast(OT, *(const u4 *)(kbase + i * I::KTILE + 32 * kb));
+        const QT kop = __builtin_bit_cast(QT, *(const u4 *)(kbase + i * I::KTILE + 32 * kb));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-          if constexpr (F16)
+          if constexpr (QF16)
             S[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qv[rb][kb], S[i][rb], 0, 0, 0);
           else
             S[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qv[rb][kb], S[i][rb], 0, 0, 0);
+        }
+      }
+    }
+    if constexpr (QUANT) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const f4 scr = *(const f4 *)(mult + ((2 * pr + i) * NG + NG - 1) * 16 + 4 * jj);
+        const BT aop = __builtin_bit_cast(BT, *(const u2 *)(bias + ((2 * pr + i) * 16 + col) * 16 + 4 * jj));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          f4 c;
+          if constexpr (BF16_BIAS) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) c[r] = __builtin_fmaf(S[i][rb][r], scr[r], -mb[rb]);
+            c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop, qop[rb], c, 0, 0, 0);
+          } else if (wide) {  // uniform: rows outside f16 range in this wave (rare)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              c[r] = __builtin_fmaf(S[i][rb][r], scr[r] * dn[rb], -mb[rb] * dn[rb]);
+            c = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, qop[rb], c, 0, 0, 0);
+            c *= ue[rb];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) c[r] = __builtin_fmaf(S[i][rb][r], scr[r], -mb[rb]);
+            c = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, qop[rb], c, 0, 0, 0);
+          }
+          S[i][rb] = c;
         }
       }
     }
@@ -521,7 +692,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = __builtin_fmaf(S[i][rb][r], rsc[rb], -mb[rb]);
+        for (int r = 0; r < 4; ++r)
+          v[rb][4 * i + r] = QUANT ? S[i][rb][r] : __builtin_fmaf(S[i][rb][r], rsc, -mb[rb]);
       if (!fast) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -549,7 +721,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[rb][e] -= shift;
           m[rb] = mn;
-          lsum[rb] *= alpha;
+          if constexpr (MSUM) OS[rb] *= alpha;
+          else lsum[rb] *= alpha;
 #pragma unroll
           for (int n = 0; n < NB; ++n) O[rb][n] *= alpha;
         }
@@ -560,20 +733,20 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // pages also pack the rounding error Plo (P = hi + lo: 16 significant bits,
   // where one bf16 alone, 2^-9 relative, times values of outlier channels
   // exceeds the output tolerance on short spans)
-  auto probs = [&](const float (&v)[RB][8], OT (&P)[RB], OT (&Plo)[RB]) __attribute__((always_inline)) {
+  auto probs = [&](const float (&v)[RB][8], PT (&P)[RB], PT (&Plo)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(v[rb][e]);
-      lsum[rb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-      if constexpr (F16) {
+      if constexpr (!MSUM) lsum[rb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      if constexpr (PF16) {
         P[rb] = h8{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
                    (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
       } else {
         P[rb] = b8{(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3],
                    (__bf16)p[4], (__bf16)p[5], (__bf16)p[6], (__bf16)p[7]};
-        OT lo;
+        PT lo;
 #pragma unroll
         for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(p[e] - (float)P[rb][e]);
         Plo[rb] = lo;
@@ -581,20 +754,27 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     }
   };
   // O^T += V^T.P^T over the step's 32 tokens
-  auto pv = [&](const uint16_t *img, int pr, const OT (&P)[RB], const OT (&Plo)[RB]) __attribute__((always_inline)) {
+  auto pv = [&](const uint16_t *img, int pr, const PT (&P)[RB], const PT (&Plo)[RB]) __attribute__((always_inline)) {
     const uint16_t *vbase = img + I::K_ELEMS + col * I::VROW + 32 * pr + 8 * jj;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      const OT vop = __builtin_bit_cast(OT, *(const u4 *)(vbase + 16 * n * I::VROW));
+      const PT vop = __builtin_bit_cast(PT, *(const u4 *)(vbase + 16 * n * I::VROW));
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        if constexpr (F16)
+        if constexpr (PF16)
           O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, P[rb], O[rb][n], 0, 0, 0);
         else {
           O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, P[rb], O[rb][n], 0, 0, 0);
           O[rb][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, Plo[rb], O[rb][n], 0, 0, 0);
         }
       }
+    }
+    if constexpr (MSUM) {
+      const _Float16 one = col == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+      const h8 ones = {one, one, one, one, one, one, one, one};
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        OS[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, P[rb], OS[rb], 0, 0, 0);
     }
   };
 
@@ -617,6 +797,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
     const uint16_t *img = stage[buf];
+    const float *mult = s_mult[buf];
+    const uint16_t *bias = s_bias[buf];
     // the stage's tile flags (uniform bit mask)
     int okv = 0;
 #pragma unroll
@@ -631,12 +813,12 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     constexpr int NPAIR = kStageTiles / 2;
     f4 S[2][2][RB];
     float mb[2][RB], v[RB][8];
-    OT P[RB], Plo[RB];
-    qk(img, 0, S[0], mb[0]);
+    PT P[RB], Plo[RB];
+    qk(img, mult, bias, 0, S[0], mb[0]);
 #pragma unroll
     for (int pr = 0; pr < NPAIR; ++pr) {
       scores(S[pr & 1], mb[pr & 1], s, pr, okv, v);
-      if (pr + 1 < NPAIR) qk(img, pr + 1, S[(pr + 1) & 1], mb[(pr + 1) & 1]);
+      if (pr + 1 < NPAIR) qk(img, mult, bias, pr + 1, S[(pr + 1) & 1], mb[(pr + 1) & 1]);
       probs(v, P, Plo);
       pv(img, pr, P, Plo);
       if (pr == 0) {
@@ -652,8 +834,12 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // ---- epilogue: fold the 4 jj lanes of a column, normalise, write
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
-    lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
+    if constexpr (MSUM) {
+      lsum[rb] = __shfl(OS[rb][0], col, 64);  // row 0 lives in lane (col, jj = 0)
+    } else {
+      lsum[rb] += __shfl_xor(lsum[rb], 16, 64);
+      lsum[rb] += __shfl_xor(lsum[rb], 32, 64);
+    }
     const int row = rblk * ROWS + wv * 16 * RB + rb * 16 + col;
     if (row >= a.rows) continue;
     const int qi = row / a.gqa, h = kh * a.gqa + row % a.gqa;
@@ -693,8 +879,9 @@ typedef void (*PrefillKernel)(AttnArgs);
 
 template <bool SHARE>
 static PrefillKernel select_prefill(const Geo &g) {
-#define PKV_Q(BITS_, DP_, G_) \
-  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_) return prefill_kernel<BITS_, DP_, G_, 1, SHARE>;
+#define PKV_Q(BITS_, DP_, G_)                                                              \
+  if (g.bits == BITS_ && g.dp == DP_ && g.group == G_)                                     \
+    return g.float_kind == 1 ? prefill_kernel<BITS_, DP_, G_, 1, SHARE> : prefill_kernel<BITS_, DP_, G_, 0, SHARE>;
   PKV_Q(8, 64, 32) PKV_Q(8, 64, 64)
   PKV_Q(8, 128, 32) PKV_Q(8, 128, 64) PKV_Q(8, 128, 128)
   PKV_Q(8, 256, 32) PKV_Q(8, 256, 64) PKV_Q(8, 256, 128)

@@ -449,29 +449,21 @@ QUERY_SCALE_CASES = {
     "decode_int4_g32": dict(name="c3", batch=2, lengths=(700, 40), group_size=32),
     "verify_int8_rows20": dict(name="c4", batch=3, length_range=(10, 400), shared_prefix_pages=0),
     "prefill_int8": dict(name="c5", batch=2, lengths=(200, 70), num_queries=64, append_tokens=64),
+    # four and eight quantization groups per row (bias parts: 3 and 2 per group)
+    "prefill_int4_g32": dict(name="c5", batch=2, lengths=(150, 40), num_queries=48,
+                             append_tokens=48, bits=4, group_size=32),
+    "prefill_int8_d256_g32": dict(name="c5", batch=2, lengths=(120, 33), num_queries=40,
+                                  append_tokens=40, head_dim=256, group_size=32),
 }
-
-
-# The chunked-prefill kernel dequantizes K to f16 once per stage (one
-# rounding, relative 2^-11), which is what keeps it MFMA-bound; the query
-# operand is exact and scale*log2(e) is applied to the f32 scores.  Its score
-# error still grows with |q|*|k|: the 10x queries pass the 2e-2 bar, 30x and
-# beyond do not.  The decode and verify kernels keep codes exact and apply
-# scales in f32, at any magnitude.
-_PREFILL_LIMIT = pytest.mark.xfail(
-    strict=True, reason="prefill kernel: K dequantized to f16, error grows with |q|*|k| "
-                        "(within the bar up to ~10x N(0,1) queries)")
 
 
 def _scale_params():
     params = []
     for case in sorted(QUERY_SCALE_CASES):
         for factor in (10.0, 30.0, 300.0, 1e6, 3e-6):
-            large = case.startswith("prefill") and factor >= 30
             if factor == 10.0 and not case.startswith("prefill"):
                 continue
-            params.append(pytest.param(case, factor, marks=[_PREFILL_LIMIT] if large else [],
-                                       id=f"{case}-{factor:g}"))
+            params.append(pytest.param(case, factor, id=f"{case}-{factor:g}"))
     return params
 
 
