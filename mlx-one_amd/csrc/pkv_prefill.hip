@@ -77,9 +77,12 @@ struct StageImage {
 // Score metadata of quantized K tiles (next to the stage image), per tile:
 //   mult [NG][16 tokens] f32: scale_g / scale_{g+1} for g < NG - 1, then
 //        scale_last * softmax scale * log2(e); 0 for absent tokens
-//   bias [16 tokens][16 slots] f16: the A operand of the bias MFMA, slot k
-//        holding bias_{k / SPG} (SPG slots per group, one per part of the
-//        query's group sum), 0 past the groups and for absent tokens
+//   bias [4 slot quads][16 tokens][4 slots] 16-bit: the A operand of the
+//        bias MFMA, slot k holding bias_{k / SPG} (SPG slots per group, one
+//        per part of the query's group sum), 0 past the groups and for absent
+//        tokens.  Lane (col, jj) reads quad jj of token col: each 16-lane
+//        group reads 128 contiguous bytes (no bank conflicts; a token-major
+//        layout, 32 bytes per lane apart, conflicted four ways)
 // SPG: 3 parts (33 significant bits) while 3 * NG <= 16, else 2 (22 bits).
 constexpr int bias_parts(int ng) { return 3 * ng <= 16 ? 3 : 2; }
 
@@ -550,7 +553,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
               if ((k & 3) == i) bo[i] = (k >> 2) == jj ? part[BF16_BIAS && pt >= 3] : bo[i];
           }
         }
-        *(u2 *)(s_bias[dst] + (wv * 16 + col) * 16 + 4 * jj) = __builtin_bit_cast(u2, bo);
+        *(u2 *)(s_bias[dst] + ((wv * 4 + jj) * 16 + col) * 4) = __builtin_bit_cast(u2, bo);
       }
 #pragma unroll
       for (int n = 0; n < (k_half ? 0 : NB); ++n) {
@@ -653,7 +656,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const f4 scr = *(const f4 *)(mult + ((2 * pr + i) * NG + NG - 1) * 16 + 4 * jj);
-        const BT aop = __builtin_bit_cast(BT, *(const u2 *)(bias + ((2 * pr + i) * 16 + col) * 16 + 4 * jj));
+        const BT aop = __builtin_bit_cast(BT, *(const u2 *)(bias + (((2 * pr + i) * 4 + jj) * 16 + col) * 4));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           f4 c;
