@@ -12,10 +12,12 @@ before timing.  The timed steps are captured as one HIP graph and replayed
 once untimed, then once timed for the step time (``--eager`` launches them
 from the host instead); ``roofline.achieved`` divides the algorithmic bytes
 (or flops) of a launch by its average duration: HIP events around a graph
-replay of the timed steps' attention launches, over the launch count
-(``roofline.kernel_timing``; beside it: the launch inside the step, step
-graph time minus an append-only graph's, and events around each launch of a
-host-launched pass, which add their own overhead).  For the HBM-bound
+replay of the timed steps' attention launches, over the launch count, with
+the stream held by a spin kernel while the host submits the graph, so that
+the span holds GPU work only (``roofline.kernel_timing``; beside it: the
+launch inside the step, step graph time minus an append-only graph's, and
+events around each launch of a host-launched pass, which add their own
+overhead).  For the HBM-bound
 decode workloads ``roofline.read_probe`` times ``pkv_read_probe`` -- a kernel
 that only reads every byte of the pages the step's sequences hold, at the
 same wave count -- the same way, and ``roofline.frac_of_read_probe`` compares
@@ -44,6 +46,25 @@ MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA (no sparsity)
 # GPU clock cycles the stream is held per step of the event pass (~100 us of
 # host enqueue time per step at ~2.4 GHz)
 SLEEP_CYCLES_PER_STEP = 240_000
+# GPU clock cycles the stream is held before a timed graph replay (~1 ms): the
+# host submits the graph's launches meanwhile, so the first one starts right
+# after the opening event and the span holds GPU work only
+GRAPH_HOLD_CYCLES = 2_400_000
+
+
+def held_replay(graph, device):
+    """Replay ``graph`` between two HIP events, the stream held by a bounded
+    spin kernel while the host submits it; returns the span in ms."""
+    import torch
+
+    stream = torch.cuda.current_stream(device)
+    span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    torch.cuda._sleep(GRAPH_HOLD_CYCLES)
+    span[0].record(stream)
+    graph.replay()
+    span[1].record(stream)
+    torch.cuda.synchronize()
+    return span[0].elapsed_time(span[1])
 
 
 def measured_traffic(workload):
@@ -494,12 +515,7 @@ def read_probe(lib, fmt, layers, table, lengths, waves, steps, device):
             launch(i)
     graph.replay()
     torch.cuda.synchronize()
-    span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    span[0].record(torch.cuda.current_stream(device))
-    graph.replay()
-    span[1].record(torch.cuda.current_stream(device))
-    torch.cuda.synchronize()
-    ms = span[0].elapsed_time(span[1]) / steps
+    ms = held_replay(graph, device) / steps
     return ms, int(ids.numel()) * fmt.page_bytes, int(ids.numel())
 
 
@@ -678,12 +694,9 @@ def main(argv=None):
                   file=sys.stderr)
             graph = attn_graph = append_graph = None
     torch.cuda.synchronize()
-    step_span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     t0 = time.perf_counter()
     if graph is not None:
-        step_span[0].record(torch.cuda.current_stream(device))
         graph.replay()
-        step_span[1].record(torch.cuda.current_stream(device))
     else:
         for i in range(args.steps):
             step(args.warmup + i, events[i])
@@ -691,18 +704,10 @@ def main(argv=None):
     wall = time.perf_counter() - t0
     span_ms = append_ms = None
     if graph is not None:
-        span = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        span[0].record(torch.cuda.current_stream(device))
-        attn_graph.replay()
-        span[1].record(torch.cuda.current_stream(device))
-        torch.cuda.synchronize()
-        span_ms = span[0].elapsed_time(span[1]) / args.steps
+        span_ms = held_replay(attn_graph, device) / args.steps
         if append_graph is not None:
-            span[0].record(torch.cuda.current_stream(device))
-            append_graph.replay()
-            span[1].record(torch.cuda.current_stream(device))
-            torch.cuda.synchronize()
-            append_ms = span[0].elapsed_time(span[1]) / args.steps
+            append_ms = held_replay(append_graph, device) / args.steps
+            step_graph_ms = held_replay(graph, device) / args.steps
         # Hold the stream with a bounded spin kernel while the host enqueues
         # the per-launch pass, so that its events bracket GPU work only.
         torch.cuda._sleep(int(args.steps * SLEEP_CYCLES_PER_STEP))
@@ -712,8 +717,9 @@ def main(argv=None):
     per_launch_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
     attn_ms = span_ms if span_ms is not None else per_launch_ms
     ms_per_step = wall / args.steps * 1e3
-    timing = ("HIP events around a graph replay of the timed steps' attention launches, "
-              "divided by the launch count" if span_ms is not None else
+    timing = ("HIP events around a graph replay of the timed steps' attention launches "
+              "(stream held while the host submits it), divided by the launch count"
+              if span_ms is not None else
               "HIP events per launch in the timed host-launched steps")
     timed = plans[args.warmup:]
     mean_lens = np.mean([p[3] for p in timed], axis=0)
@@ -745,6 +751,8 @@ def main(argv=None):
     elif attn_ms:
         if fused:   # the launch also reads the new K/V rows
             attn_bytes = step_bytes
+        rows = w.num_queries * w.heads // w.kv_heads
+        valu = args.decode_kernel == "valu" and w.bits != 16 and rows <= 4 and not fused
         achieved = attn_bytes / (attn_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -752,9 +760,7 @@ def main(argv=None):
                     "kernel": ("pkv_append_paged_attention (attn_kernel with the fused "
                                "append + merge_kernel)" if fused else
                                "pkv_paged_attention ({} + merge_kernel)".format(
-                                   "valu_kernel" if args.decode_kernel == "valu" and
-                                   w.bits != 16 and w.num_queries * w.heads // w.kv_heads <= 4
-                                   else "attn_kernel")),
+                                   "valu_kernel" if valu else "attn_kernel")),
                     "kernel_timing": timing,
                     "kernel_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes)}
     if roofline is not None and roofline["bound"] == "hbm" and graph is not None:
@@ -775,8 +781,7 @@ def main(argv=None):
         if append_ms is not None:
             # the launch inside the step (after its append): step graph time
             # minus an append-only graph's
-            step_ms = step_span[0].elapsed_time(step_span[1]) / args.steps
-            roofline["kernel_ms_in_step"] = round(step_ms - append_ms, 5)
+            roofline["kernel_ms_in_step"] = round(step_graph_ms - append_ms, 5)
     kv = {8: "int8", 4: "4-bit", 16: "bf16"}[w.bits]
     shape = ("Llama-3-8B shape, " if (w.heads, w.kv_heads, w.head_dim) == (32, 8, 128) else "")
     if w.widths:
