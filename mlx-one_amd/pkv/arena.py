@@ -95,6 +95,7 @@ class SegmentedPageArena(BlockPool):
         self.replacement_peak_bytes = 0
         self._tables = weakref.WeakSet()
         self._leases = []
+        self._segment_pages = {}   # occupied segment id -> live pages in it (stats)
 
     # -- pools ---------------------------------------------------------------
     def pool_for(self, layout) -> DevicePagePool:
@@ -112,10 +113,20 @@ class SegmentedPageArena(BlockPool):
         pool = self.pool_for(layout)
         if self.nbytes + pool.page_bytes > self.capacity_bytes:
             raise CacheCapacityError("segmented KV arena is full")
-        return pool.take(), pool.page_bytes
+        page = pool.take()
+        sid = (pool.ordinal << 32) | (page // SEGMENT_PAGES)
+        self._segment_pages[sid] = self._segment_pages.get(sid, 0) + 1
+        return page, pool.page_bytes
 
     def _reclaim_page(self, layout, page):
-        self.pools[layout].give(page)
+        pool = self.pools[layout]
+        sid = (pool.ordinal << 32) | (page // SEGMENT_PAGES)
+        left = self._segment_pages[sid] - 1
+        if left:
+            self._segment_pages[sid] = left
+        else:
+            del self._segment_pages[sid]
+        pool.give(page)
 
     def _store_state(self, block, state):
         """Write float K/V page tensors ``[1, HK, P, D]`` (quantizing if the layout says so)."""
@@ -174,9 +185,8 @@ class SegmentedPageArena(BlockPool):
 
     def stats(self):
         result = super().stats()
-        payload = sum(b.nbytes * b.token_count // max(self.block_tokens, 1)
-                      for b in self._blocks.values())
-        result.update(arena_version=ARENA_VERSION, segment_count=len(self.segments),
+        payload = self.payload_nbytes()
+        result.update(arena_version=ARENA_VERSION, segment_count=len(self._segment_pages),
                       segment_capacity_pages=SEGMENT_PAGES, page_payload_bytes=payload,
                       unused_segment_bytes=self.allocated_nbytes - payload,
                       table_bytes=sum(t.table_bytes for t in list(self._tables)),
@@ -191,6 +201,7 @@ class SegmentedPageArena(BlockPool):
             super().clear()
             self.pools.clear()
             self._tables = weakref.WeakSet()
+            self._segment_pages = {}
 
 
 class PersistentPageTable:

@@ -122,6 +122,27 @@ class BlockPool:
         self._generation = 0
         self._lock = threading.RLock()
         self._live_nbytes = 0      # sum of nbytes over live blocks, kept incrementally
+        self._reset_counts()
+
+    # -- running statistics: each block's share, added and taken back around
+    # every change of its references, pins or token count, so that stats()
+    # costs the same whatever the number of blocks --------------------------------
+    def _reset_counts(self):
+        self._n_live = self._n_pinned = self._n_shared = 0
+        self._b_pinned = self._b_evictable = self._b_shared = self._b_payload = 0
+
+    def _count(self, b, sign):
+        if b.references > 0:
+            self._n_live += sign
+        if b.references > 1:
+            self._n_shared += sign
+            self._b_shared += sign * b.nbytes * (b.references - 1)
+        if b.pins > 0:
+            self._n_pinned += sign
+            self._b_pinned += sign * b.nbytes
+        if b.references == 0 and b.pins == 1:
+            self._b_evictable += sign * b.nbytes
+        self._b_payload += sign * (b.nbytes * b.token_count // max(self.block_tokens, 1))
 
     # -- identities --------------------------------------------------------
     def _identity(self, slot):
@@ -141,15 +162,17 @@ class BlockPool:
         with self._lock:
             page, nbytes = self._place(layout)
             block_id = self._identity(page)
-            self._blocks[block_id] = CacheBlock(block_id, token_count, page=page, layout=layout,
-                                                nbytes=nbytes)
+            block = CacheBlock(block_id, token_count, page=page, layout=layout, nbytes=nbytes)
+            self._blocks[block_id] = block
             self._live_nbytes += nbytes
+            self._count(block, 1)
             if state is not None:
                 try:
-                    self._store_state(self._blocks[block_id], state)
+                    self._store_state(block, state)
                 except BaseException:
                     del self._blocks[block_id]
                     self._live_nbytes -= nbytes
+                    self._count(block, -1)
                     self._reclaim_page(layout, page)
                     raise
             return block_id
@@ -159,29 +182,49 @@ class BlockPool:
 
     def acquire(self, block_id):
         with self._lock:
-            self._require(block_id).references += 1
+            block = self._require(block_id)
+            self._count(block, -1)
+            block.references += 1
+            self._count(block, 1)
 
     def release(self, block_id):
         with self._lock:
             block = self._require(block_id)
             if block.references < 1:
                 raise CacheCorruptionError("KV block reference count became negative")
+            self._count(block, -1)
             block.references -= 1
             if block.references == 0 and block.pins == 0:
                 self._drop(block)
+            else:
+                self._count(block, 1)
 
     def pin(self, block_id):
         with self._lock:
-            self._require(block_id).pins += 1
+            block = self._require(block_id)
+            self._count(block, -1)
+            block.pins += 1
+            self._count(block, 1)
 
     def unpin(self, block_id):
         with self._lock:
             block = self._require(block_id)
             if block.pins < 1:
                 raise CacheCorruptionError("KV block pin count became negative")
+            self._count(block, -1)
             block.pins -= 1
             if block.pins == 0 and block.references == 0:
                 self._drop(block)
+            else:
+                self._count(block, 1)
+
+    def set_token_count(self, block, token_count):
+        """Change a live block's token count (a tail page filling, or rolled
+        back), keeping the running statistics."""
+        with self._lock:
+            self._count(block, -1)
+            block.token_count = token_count
+            self._count(block, 1)
 
     def seal(self, block_id):
         with self._lock:
@@ -195,6 +238,7 @@ class BlockPool:
             return self._require(block_id)
 
     def _drop(self, block):
+        # its share is already taken back by the caller (release / unpin)
         del self._blocks[block.block_id]
         self._live_nbytes -= block.nbytes
         self._reclaim_page(block.layout, block.page)
@@ -207,21 +251,26 @@ class BlockPool:
 
     def stats(self):
         with self._lock:
-            blocks = list(self._blocks.values())
             return {
-                "block_total": len(blocks),
+                "block_total": len(self._blocks),
                 "block_free": 0,
-                "block_live": sum(b.references > 0 for b in blocks),
-                "block_prefix": sum(b.pins > 0 for b in blocks),
-                "block_shared": sum(b.references > 1 for b in blocks),
-                "block_pinned": sum(b.pins > 0 for b in blocks),
+                "block_live": self._n_live,
+                "block_prefix": self._n_pinned,
+                "block_shared": self._n_shared,
+                "block_pinned": self._n_pinned,
                 "physical_bytes": self.allocated_nbytes,
-                "live_bytes": sum(b.nbytes for b in blocks),
-                "retained_free_bytes": self.allocated_nbytes - sum(b.nbytes for b in blocks),
-                "evictable_bytes": sum(b.nbytes for b in blocks if b.references == 0 and b.pins == 1),
-                "shared_page_savings_bytes": sum(b.nbytes * max(b.references - 1, 0) for b in blocks),
-                "pinned_bytes": sum(b.nbytes for b in blocks if b.pins),
+                "live_bytes": self._live_nbytes,
+                "retained_free_bytes": self.allocated_nbytes - self._live_nbytes,
+                "evictable_bytes": self._b_evictable,
+                "shared_page_savings_bytes": self._b_shared,
+                "pinned_bytes": self._b_pinned,
             }
+
+    def payload_nbytes(self):
+        """Bytes of the tokens the live blocks hold (nbytes * tokens / block
+        width per block)."""
+        with self._lock:
+            return self._b_payload
 
     @property
     def allocated_nbytes(self):
@@ -231,6 +280,7 @@ class BlockPool:
         with self._lock:
             self._blocks.clear()
             self._live_nbytes = 0
+            self._reset_counts()
             self._next_id = 0
             self._epoch = uuid.uuid4().int
 

@@ -123,7 +123,7 @@ class PagedKVCache:
                 if tail.references != 1 or tail.pins:
                     raise ValueError("mutable paged tail is shared")
                 fill = min(self.block_tokens - tail.token_count, width - cursor)
-                tail.token_count += fill
+                self.pool.set_token_count(tail, tail.token_count + fill)
             cursor += fill
             self._offset += fill
             if tail.token_count == self.block_tokens:
@@ -234,7 +234,7 @@ class PagedKVCache:
         while len(self._blocks) > count:
             self._blocks.pop().close()
         if tail is not None:
-            tail.token_count = tail_tokens
+            self.pool.set_token_count(tail, tail_tokens)
             tail.immutable = sealed
         self._offset = offset
         self.page_table.truncate(count)

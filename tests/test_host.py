@@ -217,3 +217,64 @@ def test_page_pool_stays_within_the_byte_budget_and_reuses_lowest_ids():
     for i in sorted((7, 3, 5), reverse=True):
         cache._blocks.pop(i).close()
     assert [pool.take() for _ in range(3)] == sorted(freed)
+
+
+def _recount(arena):
+    """The pool's statistics recomputed from every live block."""
+    blocks = list(arena._blocks.values())
+    nbytes = sum(b.nbytes for b in blocks)
+    return {"block_total": len(blocks), "block_live": sum(b.references > 0 for b in blocks),
+            "block_prefix": sum(b.pins > 0 for b in blocks),
+            "block_shared": sum(b.references > 1 for b in blocks),
+            "block_pinned": sum(b.pins > 0 for b in blocks), "live_bytes": nbytes,
+            "retained_free_bytes": arena.allocated_nbytes - nbytes,
+            "evictable_bytes": sum(b.nbytes for b in blocks if b.references == 0 and b.pins == 1),
+            "shared_page_savings_bytes": sum(b.nbytes * max(b.references - 1, 0) for b in blocks),
+            "pinned_bytes": sum(b.nbytes for b in blocks if b.pins),
+            "page_payload_bytes": sum(b.nbytes * b.token_count // arena.block_tokens
+                                      for b in blocks),
+            "segment_count": len(arena.segments)}
+
+
+def test_running_pool_statistics_match_a_recount():
+    """stats() is kept incrementally (it runs every runner step): through
+    appends that fill and seal tails, forks, pins of evicted-to-prefix pages,
+    rollbacks of partial tails and releases, it equals a recount of the live
+    blocks."""
+    rng = np.random.default_rng(7)
+    arena = SegmentedPageArena(2**40, block_tokens=16, device="cpu")
+    caches = [_cache(arena) for _ in range(4)]
+    held, pinned = [], []
+    for step in range(120):
+        op = int(rng.integers(6))
+        c = caches[int(rng.integers(len(caches)))]
+        if op <= 1:
+            _plan(c, int(rng.integers(1, 40)))
+        elif op == 2 and any(r.block.immutable for r in c._blocks):
+            sealed = [r for r in c._blocks if r.block.immutable]     # a mutable tail stays unshared
+            held.append(sealed[int(rng.integers(len(sealed)))].fork())
+        elif op == 3 and held:
+            ref = held.pop(int(rng.integers(len(held))))
+            arena.pin(ref.block_id)
+            ref.close()                                  # pinned only: evictable
+            if rng.integers(2):
+                arena.unpin(ref.block_id)
+            else:
+                pinned.append(ref.block_id)
+        elif op == 4:
+            mark = c.checkpoint()
+            _plan(c, int(rng.integers(1, 20)))
+            c.rollback(mark)
+        elif op == 5 and rng.integers(4) == 0:
+            c.reset()
+        got = arena.stats()
+        want = _recount(arena)
+        assert {k: got[k] for k in want} == want, step
+    for ref in held:
+        ref.close()
+    for c in caches:
+        c.reset()
+    for block_id in pinned:
+        arena.unpin(block_id)
+    assert arena.stats()["block_total"] == 0 and arena.stats()["page_payload_bytes"] == 0
+    assert _recount(arena)["live_bytes"] == 0 == arena.stats()["evictable_bytes"]
