@@ -96,6 +96,13 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Query rows of sequence b live in this launch: 0 for a sequence of a mixed
 // batch that the decode kernel serves (narrow_q > 0, width at most narrow_q).
+// f32 -> bf16 bits on v_cvt_pk_bf16_f32 (round to nearest even): for the
+// values an f16 holds (never f32 denormals) the bits of f32_to_bf16_bits,
+// without its software NaN branch.
+__device__ __forceinline__ uint16_t bf16_bits_cvt(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
 __device__ __forceinline__ int prefill_width(const AttnArgs &a, int b) {
   return a.widths ? (a.narrow_q > 0 && a.widths[b] <= a.narrow_q ? 0 : a.widths[b]) : a.nq;
 }
@@ -196,7 +203,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   constexpr bool BF16_BIAS = QUANT && 6 * NG <= 16;
   typedef typename std::conditional<BF16_BIAS, s4, h4>::type BT;  // bias MFMA operand
 
-  __shared__ __attribute__((aligned(16))) int s_valid[2][kStageTiles];
+  // tile flags of a stage image, one byte each (0 or 1), read as words
+  __shared__ __attribute__((aligned(16))) uint8_t s_valid[2][kStageTiles];
   __shared__ int s_lim[2][kPrefillWaves];
   __shared__ int64_t s_zero[SHARE ? 2 : 1];  // zero share: first row, end
   __shared__ __attribute__((aligned(16))) uint16_t stage[2][I::ELEMS];
@@ -527,7 +535,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
           if ((gi & 3) != jj) continue;
-          const float mv = gi + 1 < NG ? scl[gi] / scl[gi + 1 < NG ? gi + 1 : gi]
+          // (scales are at least 1e-6: the reciprocal is within 1 ulp)
+          const float mv = gi + 1 < NG ? scl[gi] * __builtin_amdgcn_rcpf(scl[gi + 1 < NG ? gi + 1 : gi])
                                        : scl[gi] * a.scale_log2;
           mrow[gi * 16] = tv ? mv : 0.0f;
         }
@@ -541,9 +550,9 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
           short part[2] = {(short)bb, (short)bb};
           if constexpr (BF16_BIAS) {
             const float bf = f16_bits_to_f32(bb);
-            const uint16_t hi = f32_to_bf16_bits(bf);
+            const uint16_t hi = bf16_bits_cvt(bf);
             part[0] = (short)hi;
-            part[1] = (short)f32_to_bf16_bits(bf - __uint_as_float((uint32_t)hi << 16));
+            part[1] = (short)bf16_bits_cvt(bf - __uint_as_float((uint32_t)hi << 16));
           }
 #pragma unroll
           for (int pt = 0; pt < SPG; ++pt) {
@@ -584,7 +593,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
         *(u2 *)(vdst + 16 * n * I::VROW) = v;
       }
     }
-    if (!k_half && lane == 0) s_valid[dst][wv] = r_ok;
+    if (!k_half && lane == 0) s_valid[dst][wv] = r_ok ? 1 : 0;
   };
 
   // Row sums of P: f16 P operands (quantized and f16 pages) sum on the MFMA
@@ -592,12 +601,16 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // the same rounded P the output accumulates; bf16 pages (P = hi + lo) sum
   // the f32 probabilities on the VALU.
   constexpr bool MSUM = PF16;
-  float m[RB], lsum[RB];
+  // m: the running maximum in the exp2 domain, 0 before the row has seen a
+  // token; thr: the rescale threshold over m, -inf until then (so that the
+  // first finite score sets m), kTau after.
+  float m[RB], thr[RB], lsum[RB];
   f4 OS[MSUM ? RB : 1];
   f4 O[RB][NB];  // O^T[d = 16n + 4jj + r][column]
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    m[rb] = -INFINITY;
+    m[rb] = 0.0f;
+    thr[rb] = -INFINITY;
     lsum[rb] = 0.0f;
     if constexpr (MSUM) OS[rb] = f4{0, 0, 0, 0};
 #pragma unroll
@@ -622,7 +635,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
                 f4 (&S)[2][RB], float (&mb)[RB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      mb[rb] = m[rb] == -INFINITY ? 0.0f : m[rb];
+      mb[rb] = m[rb];
 #pragma unroll
       for (int i = 0; i < 2; ++i) S[i][rb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -708,8 +721,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
           }
       }
       mx[rb] = max8(v[rb]);
-      // before any token is seen every finite score resets the max
-      need |= mx[rb] > (m[rb] == -INFINITY ? -INFINITY : kTau);
+      // before any token is seen every finite score sets the max
+      need |= mx[rb] > thr[rb];
     }
     if (__any(need)) {
 #pragma unroll
@@ -717,10 +730,12 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
         float tm = mx[rb];
         tm = __builtin_elementwise_maximum(tm, __shfl_xor(tm, 16, 64));
         tm = __builtin_elementwise_maximum(tm, __shfl_xor(tm, 32, 64));
-        const float mn = fmaxf(m[rb], tm + mb[rb]);
-        if (mn != -INFINITY && mn != m[rb]) {
+        const bool first = thr[rb] == -INFINITY;  // nothing accumulated yet
+        const float mn = first ? tm + mb[rb] : fmaxf(m[rb], tm + mb[rb]);
+        if (mn != -INFINITY && (first || mn != m[rb])) {
           const float shift = mn - mb[rb];
-          const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);  // 0 when m was -inf
+          const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m[rb] - mn);
+          thr[rb] = kTau;
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[rb][e] -= shift;
           m[rb] = mn;
@@ -803,13 +818,14 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     const float *mult = s_mult[buf];
     const uint16_t *bias = s_bias[buf];
     // the stage's tile flags (uniform bit mask)
+    // (bytes b0..b3 of 0/1: w * 0x01020408 puts b_i at bit 24 + i, every
+    // other product term below bit 20 or past bit 31)
     int okv = 0;
 #pragma unroll
     for (int q4 = 0; q4 < kStageTiles / 4; ++q4) {
-      const u4 okw = *(const u4 *)&s_valid[buf][4 * q4];
-      okv |= ((okw.x != 0) | ((okw.y != 0) << 1) | ((okw.z != 0) << 2) | ((okw.w != 0) << 3)) << (4 * q4);
+      const uint32_t w = __builtin_amdgcn_readfirstlane(*(const uint32_t *)&s_valid[buf][4 * q4]);
+      okv |= (int)(((w * 0x01020408u) >> 24) & 0xFu) << (4 * q4);
     }
-    okv = __builtin_amdgcn_readfirstlane(okv);
     // steps over tile pairs; pair pr+1's QK MFMAs are issued before pair
     // pr's exponentials, the conversion halves sit beside the first two
     // pairs' PV MFMAs
