@@ -711,12 +711,13 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
         for (int r = 0; r < 4; ++r)
           v[rb][4 * i + r] = QUANT ? S[i][rb][r] : __builtin_fmaf(S[i][rb][r], rsc, -mb[rb]);
       if (!fast) {
+        // token (ta + i) * 16 + 4jj + r is visible when i * 16 + r <= rel
+        const int rel = lim[rb] - ta * PKV_TILE - 4 * jj;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int tok = (ta + i) * PKV_TILE + 4 * jj + r;
-            const bool vis = (i ? okb : oka) && tok <= lim[rb];
+            const bool vis = (i ? okb : oka) && i * PKV_TILE + r <= rel;
             v[rb][4 * i + r] = vis ? v[rb][4 * i + r] : -INFINITY;
           }
       }
