@@ -83,6 +83,12 @@ constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
 // Two-row-block kernels dequantize quantized V tiles in registers (see attn_kernel).
 constexpr bool kDequantRows = true;
 
+// Waves per run: two-row-block kernels (17-32 query rows per KV head) give
+// each run of the split to a workgroup of this many waves, which share its
+// iterations round robin and combine their states in LDS at each piece's
+// end; other kernels run one wave per run.
+constexpr int run_waves(int rb) { return rb == 2 ? 4 : 1; }
+
 // Tiles of a sequence: at least one, so that an empty sequence still owns a
 // piece that writes its zero output.
 __device__ __forceinline__ int seq_tiles(int len) {
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
 }
 
 template <int BITS, int DP, int G, int RB, int FK, int SLOTS, bool APPEND>
-__global__ __launch_bounds__(64)
+__global__ __launch_bounds__(64 * run_waves(RB))
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS)))) void attn_kernel(
     const AttnArgs a) {
   using C = Cfg<BITS, DP, G, RB, FK, SLOTS>;
@@ -347,7 +353,12 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   // Lane-derived values are refreshed at every piece through an opaque copy
   // of the lane id, so the compiler recomputes per-lane addresses inside the
   // piece loop instead of hoisting them all and pinning them in registers.
-  int lane = threadIdx.x;
+  // Runs of GW waves (GW > 1): wave wk of the workgroup takes iterations wk,
+  // wk + GW, ... of each piece of the run.
+  constexpr int GW = run_waves(RB);
+  static_assert(GW == 1 || (!APPEND && SLOTS == 1), "grouped runs: no fused append, one slot");
+  const int wk = GW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+  int lane = threadIdx.x & 63;
   int col, jj, slot_l, rowc;  // slot_l: this lane's column slot; rowc: its row within the slot
   auto refresh_lane = [&]() __attribute__((always_inline)) {
     asm volatile("" : "+v"(lane));
@@ -753,6 +764,81 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     }
   };
 
+  // ---- grouped runs: the GW waves' states of a piece meet in LDS, one row
+  // block at a time (32 KB at head_dim 128).  Every wave publishes its
+  // column maxima, folded row sums and O^T registers; then wave wk combines
+  // the output columns d in [16*NB/GW*wk, 16*NB/GW*(wk+1)) by log-sum-exp
+  // (a wave without a visible token holds l = 0 and weighs nothing) and
+  // writes them, normalised (whole segment) or as the run's partial.
+  constexpr int GWL = GW > 1 ? GW : 1;
+  constexpr int NBL = GW > 1 ? NB : 1;
+  __shared__ f4 s_gO[GWL][NBL][GW > 1 ? 64 : 1];
+  __shared__ float s_gm[GWL][16], s_gl[GWL][16];
+  auto group_epilogue = [&](bool whole, int slot, const float (&m)[RB], const float (&lsum)[RB],
+                            const f4 (&O)[RB][NB]) __attribute__((always_inline)) {
+    if constexpr (GW > 1) {
+      constexpr int NPW = NB / GW;
+      static_assert(NPW * GW == NB, "output column blocks per wave");
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float l = xor32_add(xor16_add(lsum[rb]));
+        if (jj == 0) {
+          s_gm[wk][col] = m[rb];
+          s_gl[wk][col] = l;
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) s_gO[wk][n][lane] = O[rb][n];
+        __syncthreads();
+        float M = -INFINITY, mk[GW], lk[GW], wt[GW];
+#pragma unroll
+        for (int k = 0; k < GW; ++k) {
+          mk[k] = s_gm[k][col];
+          lk[k] = s_gl[k][col];
+          if (lk[k] > 0.0f) M = fmaxf(M, mk[k]);
+        }
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < GW; ++k) {
+          wt[k] = lk[k] > 0.0f ? __builtin_amdgcn_exp2f(mk[k] - M) : 0.0f;
+          L += wt[k] * lk[k];
+        }
+        const int row = rb * 16 + col;
+        const bool writer = row < a.rows;
+        const int qi = row / a.gqa, h = ckh * a.gqa + row % a.gqa;
+        const float inv = 1.0f / fmaxf(L, 1e-20f);
+        uint16_t *o = a.out + (((int64_t)cb * a.heads + h) * a.nq_stride + qi) * g.dim;
+        float *pa = a.part_acc + ((int64_t)slot * a.rows + row) * DP;
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+          const int n = wk * NPW + i;
+          f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int k = 0; k < GW; ++k) v += wt[k] * s_gO[k][n][lane];
+          const int d = 16 * n + 4 * jj;
+          if (!writer) continue;
+          if (whole) {
+            if ((g.dim & 3) == 0 && d + 4 <= g.dim) {
+              u2 packed = {(uint32_t)float_to_bits(v[0] * inv, g.float_kind) |
+                               ((uint32_t)float_to_bits(v[1] * inv, g.float_kind) << 16),
+                           (uint32_t)float_to_bits(v[2] * inv, g.float_kind) |
+                               ((uint32_t)float_to_bits(v[3] * inv, g.float_kind) << 16)};
+              *(u2 *)(o + d) = packed;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (d + r < g.dim) o[d + r] = float_to_bits(v[r] * inv, g.float_kind);
+            }
+          } else {
+            *(f4 *)(pa + d) = v;
+          }
+        }
+        if (wk == 0 && writer && !whole && jj == 0)
+          *(float2 *)(a.part_ml + ((int64_t)slot * a.rows + row) * 2) = make_float2(M, L);
+        __syncthreads();  // the next row block (or piece) rewrites the LDS
+      }
+    }
+  };
+
   for (;;) {
     refresh_lane();
     // ---- start the piece: query rows and its first tiles, in flight together
@@ -771,7 +857,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         if (appends) append_fetch(cb, ckh, cL - 1);
       }
       fetch_q(cb, ckh, raw, qp);
-      cmask = plan(cta, ntl, cwin, cpid, 0, pg, tp);
+      cmask = plan(cta, ntl, cwin, cpid, wk, pg, tp);
       load_k(ckh, pg, tp, meta_at(ckh, pg, tp, g.kmeta_offset));
       load_v(ckh, pg, tp, meta_at(ckh, pg, tp, g.vmeta_offset));
       set_queries(cL, width, t1, raw, qp);
@@ -894,13 +980,13 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       const uint8_t *nmv = nullptr;
       if constexpr (MORE) {
         __builtin_amdgcn_sched_barrier(0);
-        const int first = cta + (it + 1) * SLOTS;
-        const int last = cta + min((it + 1) * SLOTS + SLOTS, ntl) - 1;
+        const int first = cta + (it + GW) * SLOTS;
+        const int last = cta + min((it + GW) * SLOTS + SLOTS, ntl) - 1;
         if ((last >> tpp_shift) - cwin > 63) {
           cwin = first >> tpp_shift;  // the iteration's tiles leave the window: slide it
           cpid = fetch_window(cb, cwin, t1);
         }
-        nmask = plan(cta, ntl, cwin, cpid, it + 1, npg, ntp);
+        nmask = plan(cta, ntl, cwin, cpid, it + GW, npg, ntp);
         load_k(ckh, npg, ntp, meta_at(ckh, npg, ntp, g.kmeta_offset));
         nmv = meta_at(ckh, npg, ntp, g.vmeta_offset);
         __builtin_amdgcn_sched_barrier(0);
@@ -1070,13 +1156,26 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         for (int j = 0; j < SLOTS; ++j) { pg[j] = npg[j]; tp[j] = ntp[j]; }
       }
     };
-    for (int it = 0; it + 1 < niters; ++it) iterate(std::true_type(), it);
-    iterate(std::false_type(), niters - 1);
+    if constexpr (GW == 1) {
+      for (int it = 0; it + 1 < niters; ++it) iterate(std::true_type(), it);
+      iterate(std::false_type(), niters - 1);
+    } else if (wk < niters) {  // (uniform per wave) a wave past the piece's iterations holds nothing
+      const int last = wk + GW * ((niters - 1 - wk) / GW);
+      for (int it = wk; it < last; it += GW) iterate(std::true_type(), it);
+      iterate(std::false_type(), last);
+    }
 
     // ---- piece epilogue: fold the 4 jj lanes of a column, then the slots of a
     // row, and write the output (whole segment) or the partial
     const bool whole = cta == 0 && ctb == cnt;
     const int slot = cfirst ? 2 * w : 2 * w + 1;
+    if constexpr (GW > 1) {
+      group_epilogue(whole, slot, m, lsum, O);
+      if (!has_next) break;
+      cb = nb; ckh = nkh; cL = nL; cnt = nnt; cseg0 = nseg0; cta = nta; ctb = ntb;
+      cfirst = false; cpid = npid;
+      continue;
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       lsum[rb] = xor32_add(xor16_add(lsum[rb]));
@@ -1768,6 +1867,10 @@ static AttnKernel select_kernel(const Geo &g, int rows, bool append = false) {
 
 bool decode_serves(const Geo &g, int rows) { return select_kernel(g, rows) != nullptr; }
 
+// Waves per run of the kernel select_kernel picks for `rows` (two row blocks
+// past 16 rows).
+static int group_of(int rows) { return run_waves(rows > 16 ? 2 : 1); }
+
 bool append_fusable(const Geo &g, int rows) { return select_kernel(g, rows, true) != nullptr; }
 
 int attention_waves(const Geo &g, int rows) {
@@ -1776,8 +1879,10 @@ int attention_waves(const Geo &g, int rows) {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64, 0) != hipSuccess) return -1;
-  return max(1, cus * per_cu);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64 * group_of(rows), 0) !=
+      hipSuccess)
+    return -1;
+  return max(1, cus * per_cu);  // resident runs
 }
 
 // The split charges each segment `lead` tiles ahead of its own, the cost of
@@ -1790,13 +1895,15 @@ int attention_waves(const Geo &g, int rows) {
 // single-token append charges 16: the wave that holds a segment's last tile
 // (the one whose run crosses into the next segment) also loads and quantizes
 // the new token before its first tiles (C2: 67.8 us against 69.0 at 8).
-int attention_lead(const Geo &, int, bool append) { return append ? 16 : 8; }
+// A run of a grouped kernel (GW waves) moves GW tiles in a wave's tile time,
+// so its lead counts GW times as many tiles.
+int attention_lead(const Geo &, int rows, bool append) { return append ? 16 : 8 * group_of(rows); }
 
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
   const AttnKernel k = select_kernel(a.g, a.rows, a.new_k != nullptr);
   if (!k) return hipErrorInvalidValue;
   if (a.waves <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64 * group_of(a.rows)), 0, stream, a);
   return hipGetLastError();
 }
 
