@@ -49,15 +49,21 @@ int geometry(const pkv_layout *layout, pkv_geometry *g) {
 constexpr int64_t kMaxRows = 1 << 24;
 
 // Attention workspace: [ml: S*rows*2 f32][acc: S*rows*DP f32] with
-// S = kSlotsPerWave * waves partial slots, each part 256-byte aligned.
+// S = kSlotsPerWave * runs partial slots (a run per wave, or per group of
+// waves for 17-32 rows), each part 256-byte aligned.
 struct WorkspaceParts {
   int64_t ml, acc, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// The runs of a launch of `waves` waves for `rows` query rows per KV head.
+int64_t attention_runs(int64_t rows, int64_t waves) {
+  return std::max<int64_t>(1, waves / pkv::attention_group((int)rows));
+}
+
 WorkspaceParts workspace_parts(const pkv_geometry &g, int64_t rows, int64_t waves) {
-  const int64_t slots = (int64_t)pkv::kSlotsPerWave * waves;
+  const int64_t slots = (int64_t)pkv::kSlotsPerWave * attention_runs(rows, waves);
   WorkspaceParts w;
   w.ml = 0;
   w.acc = align256(slots * rows * 2 * 4);
@@ -189,8 +195,14 @@ int64_t pkv_attention_workspace_bytes(const pkv_layout *layout, int32_t num_head
   if (rows > kMaxRows) return -1;
   if (!pkv::decode_serves(pkv::to_geo(g), (int)rows)) {
     // prefill kernel: no partials, except for the decode part of a mixed batch
+    // (the tiers of paged_attention_impl run in turn over one workspace)
     const int gqa = num_heads / g.hk;
-    return workspace_parts(g, (int64_t)decode_queries(g, gqa) * gqa, waves).total;
+    const int hi = decode_queries(g, gqa);
+    const int lo = std::min(hi, 4 / std::max(gqa, 1));
+    int64_t need = 0;
+    if (lo >= 1) need = workspace_parts(g, (int64_t)lo * gqa, waves).total;
+    if (hi > lo) need = std::max(need, workspace_parts(g, (int64_t)hi * gqa, waves).total);
+    return need;
   }
   return workspace_parts(g, rows, waves).total;
 }
@@ -342,7 +354,7 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     a.rows = t.nq * gqa;
     a.narrow_lo = t.lo;
     a.narrow_q = t.hi;
-    a.waves = t.waves;
+    a.waves = (int)attention_runs(a.rows, t.waves);
     a.lead = pkv::attention_lead(a.g, a.rows, fused != nullptr);
     a.part_ml = (float *)((char *)workspace + t.ws.ml);
     a.part_acc = (float *)((char *)workspace + t.ws.acc);
@@ -363,7 +375,7 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     m.dim = geo.dim;
     m.dp = geo.dp;
     m.float_kind = geo.float_kind;
-    m.waves = t.waves;
+    m.waves = a.waves;
     m.lead = a.lead;
     m.nq_stride = num_queries;
     m.narrow_lo = t.lo;
