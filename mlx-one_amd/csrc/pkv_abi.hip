@@ -57,13 +57,19 @@ struct WorkspaceParts {
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// The runs of a launch of `waves` waves for `rows` query rows per KV head.
-int64_t attention_runs(int64_t rows, int64_t waves) {
-  return std::max<int64_t>(1, waves / pkv::attention_group((int)rows));
+// The runs of a launch of `waves` waves for `rows` query rows per KV head
+// (`append`: the fused single-token form).
+int64_t attention_runs(const pkv_geometry &g, int64_t rows, int64_t waves, bool append) {
+  return std::max<int64_t>(1, waves / pkv::attention_group(pkv::to_geo(g), (int)rows, append));
 }
 
-WorkspaceParts workspace_parts(const pkv_geometry &g, int64_t rows, int64_t waves) {
-  const int64_t slots = (int64_t)pkv::kSlotsPerWave * attention_runs(rows, waves);
+// Partial space of a launch; `append` unknown (the public sizing query): the
+// larger of the forms the shape has.
+WorkspaceParts workspace_parts(const pkv_geometry &g, int64_t rows, int64_t waves, int append = -1) {
+  int64_t runs = attention_runs(g, rows, waves, append > 0);
+  if (append < 0 && pkv::append_fusable(pkv::to_geo(g), (int)rows))
+    runs = std::max(runs, attention_runs(g, rows, waves, true));
+  const int64_t slots = (int64_t)pkv::kSlotsPerWave * runs;
   WorkspaceParts w;
   w.ml = 0;
   w.acc = align256(slots * rows * 2 * 4);
@@ -262,6 +268,9 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     WorkspaceParts ws;
   };
   Part part[2];
+  // the decode kernel appends the single new token itself (else an append
+  // launch goes first): the fused form runs one wave per run
+  const int in_kernel_append = fused && !wide && pkv::append_fusable(pkv::to_geo(geo), rows) ? 1 : 0;
   int nparts = 0;
   if (!wide) {
     part[nparts++] = Part{num_queries, 0, 0, waves, {0, 0, 0}};
@@ -278,13 +287,13 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
       t.waves = pkv_attention_default_waves(layout, num_heads, t.nq, batch);
       if (t.waves <= 0) return fail(PKV_LAUNCH_FAILED, "could not query the attention kernel's occupancy");
       if (fit_waves) {
-        while (t.waves > 1 && workspace_parts(geo, trows, t.waves).total > workspace_bytes)
+        while (t.waves > 1 && workspace_parts(geo, trows, t.waves, in_kernel_append).total > workspace_bytes)
           t.waves = std::max<int64_t>(1, std::min<int64_t>(t.waves - 1,
-              (int64_t)t.waves * workspace_bytes / workspace_parts(geo, trows, t.waves).total));
+              (int64_t)t.waves * workspace_bytes / workspace_parts(geo, trows, t.waves, in_kernel_append).total));
       }
     }
     if (t.waves > (1 << 24)) return fail(PKV_INVALID_ARGUMENT, "too many waves");
-    t.ws = workspace_parts(geo, trows, t.waves);
+    t.ws = workspace_parts(geo, trows, t.waves, in_kernel_append);
     if (!workspace || workspace_bytes < t.ws.total) {
       if (!wide)
         return fail(PKV_OUT_OF_MEMORY,
@@ -354,7 +363,7 @@ int paged_attention_impl(void *stream, const pkv_layout *layout, const void *poo
     a.rows = t.nq * gqa;
     a.narrow_lo = t.lo;
     a.narrow_q = t.hi;
-    a.waves = (int)attention_runs(a.rows, t.waves);
+    a.waves = (int)attention_runs(geo, a.rows, t.waves, fused != nullptr);
     a.lead = pkv::attention_lead(a.g, a.rows, fused != nullptr);
     a.part_ml = (float *)((char *)workspace + t.ws.ml);
     a.part_acc = (float *)((char *)workspace + t.ws.acc);

@@ -83,11 +83,12 @@ constexpr int min_waves_per_simd(int bits, int dp, int g, int rb, int slots) {
 // Two-row-block kernels dequantize quantized V tiles in registers (see attn_kernel).
 constexpr bool kDequantRows = true;
 
-// Waves per run: two-row-block kernels (17-32 query rows per KV head) give
-// each run of the split to a workgroup of this many waves, which share its
-// iterations round robin and combine their states in LDS at each piece's
-// end; other kernels run one wave per run.
-constexpr int run_waves(int rb) { return rb == 2 ? 4 : 1; }
+// Waves per run: the kernels for 5-8 rows (two column slots) and 17-32 rows
+// (two row blocks) per KV head give each run of the split to a workgroup of
+// this many waves, which share its iterations round robin and combine their
+// states in LDS at each piece's end; the others (and the fused single-token
+// append) run one wave per run.
+constexpr int run_waves(int rb, int slots, bool append) { return !append && (rb == 2 || slots == 2) ? 4 : 1; }
 
 // Tiles of a sequence: at least one, so that an empty sequence still owns a
 // piece that writes its zero output.
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(64 * NW) void merge_kernel(const MergeArgs a) {
 }
 
 template <int BITS, int DP, int G, int RB, int FK, int SLOTS, bool APPEND>
-__global__ __launch_bounds__(64 * run_waves(RB))
+__global__ __launch_bounds__(64 * run_waves(RB, SLOTS, APPEND))
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS)))) void attn_kernel(
     const AttnArgs a) {
   using C = Cfg<BITS, DP, G, RB, FK, SLOTS>;
@@ -355,8 +356,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   // piece loop instead of hoisting them all and pinning them in registers.
   // Runs of GW waves (GW > 1): wave wk of the workgroup takes iterations wk,
   // wk + GW, ... of each piece of the run.
-  constexpr int GW = run_waves(RB);
-  static_assert(GW == 1 || (!APPEND && SLOTS == 1), "grouped runs: no fused append, one slot");
+  constexpr int GW = run_waves(RB, SLOTS, APPEND);
   const int wk = GW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
   int lane = threadIdx.x & 63;
   int col, jj, slot_l, rowc;  // slot_l: this lane's column slot; rowc: its row within the slot
@@ -765,9 +765,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   };
 
   // ---- grouped runs: the GW waves' states of a piece meet in LDS (64 KB at
-  // head_dim 128).  At the piece's end every wave publishes its column
-  // maxima, folded row sums and O^T registers; then wave wk combines output
-  // columns d in [16*NB/GW*wk, 16*NB/GW*(wk+1)) by log-sum-exp (a wave
+  // head_dim 128, two row blocks).  At the piece's end every wave publishes
+  // its rows' maxima, sums and O^T values as its epilogue leaves them (jj
+  // lanes and column slots folded; writer lanes); then wave wk combines
+  // output columns d in [16*NB/GW*wk, 16*NB/GW*(wk+1)) by log-sum-exp (a wave
   // without a visible token holds l = 0 and weighs nothing) and writes them,
   // normalised (whole segment) or as the run's partial.  (Deferring the
   // combine until the next piece's first loads were issued measured slower:
@@ -777,21 +778,6 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   constexpr int NBL = GW > 1 ? NB : 1;
   __shared__ f4 s_gO[GWL][RBL][NBL][GW > 1 ? 64 : 1];
   __shared__ float s_gm[GWL][RBL][16], s_gl[GWL][RBL][16];
-  auto group_publish = [&](const float (&m)[RB], const float (&lsum)[RB], const f4 (&O)[RB][NB])
-      __attribute__((always_inline)) {
-    if constexpr (GW > 1) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const float l = xor32_add(xor16_add(lsum[rb]));
-        if (jj == 0) {
-          s_gm[wk][rb][col] = m[rb];
-          s_gl[wk][rb][col] = l;
-        }
-#pragma unroll
-        for (int n = 0; n < NB; ++n) s_gO[wk][rb][n][lane] = O[rb][n];
-      }
-    }
-  };
   auto group_combine = [&](bool whole, int slot, int pb, int pkh) __attribute__((always_inline)) {
     if constexpr (GW > 1) {
       constexpr int NPW = NB / GW;
@@ -812,8 +798,8 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           wt[k] = lk[k] > 0.0f ? __builtin_amdgcn_exp2f(mk[k] - M) : 0.0f;
           L += wt[k] * lk[k];
         }
-        const int row = rb * 16 + col;
-        const bool writer = row < a.rows;
+        const int row = SLOTS > 1 ? rowc : rb * 16 + col;
+        const bool writer = slot_l == 0 && row < a.rows;
         const int qi = row / a.gqa, h = pkh * a.gqa + row % a.gqa;
         const float inv = 1.0f / fmaxf(L, 1e-20f);
         uint16_t *o = a.out + (((int64_t)pb * a.heads + h) * a.nq_stride + qi) * g.dim;
@@ -1178,14 +1164,6 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
     // row, and write the output (whole segment) or the partial
     const bool whole = cta == 0 && ctb == cnt;
     const int slot = cfirst ? 2 * w : 2 * w + 1;
-    if constexpr (GW > 1) {
-      group_publish(m, lsum, O);
-      group_combine(whole, slot, cb, ckh);
-      if (!has_next) break;
-      cb = nb; ckh = nkh; cL = nL; cnt = nnt; cseg0 = nseg0; cta = nta; ctb = ntb;
-      cfirst = false; cpid = npid;
-      continue;
-    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       lsum[rb] = xor32_add(xor16_add(lsum[rb]));
@@ -1232,6 +1210,10 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           }
           v4[r] = v;
         }
+        if constexpr (GW > 1) {  // published; the group's combine writes
+          s_gO[wk][rb][n][lane] = f4{v4[0], v4[1], v4[2], v4[3]};
+          continue;
+        }
         if (!writer) continue;
         const int d = 16 * n + 4 * jj;
         if (whole) {
@@ -1250,9 +1232,16 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           *(f4 *)(pa + d) = f4{v4[0], v4[1], v4[2], v4[3]};
         }
       }
-      if (writer && !whole && jj == 0)
+      if constexpr (GW > 1) {
+        if (jj == 0) {
+          s_gm[wk][rb][col] = mrow;
+          s_gl[wk][rb][col] = lrow;
+        }
+      } else if (writer && !whole && jj == 0) {
         *(float2 *)(a.part_ml + ((int64_t)slot * a.rows + row) * 2) = make_float2(mrow, lrow);
+      }
     }
+    if constexpr (GW > 1) group_combine(whole, slot, cb, ckh);
 
     // ---- switch to the next piece
     if (!has_next) break;
@@ -1877,11 +1866,17 @@ static AttnKernel select_kernel(const Geo &g, int rows, bool append = false) {
 
 bool decode_serves(const Geo &g, int rows) { return select_kernel(g, rows) != nullptr; }
 
-// Waves per run of the kernel select_kernel picks for `rows` (two row blocks
-// past 16 rows).
-static int group_of(int rows) { return run_waves(rows > 16 ? 2 : 1); }
+// Waves per run of the kernel select_kernel picks for `rows`: its row blocks
+// (two past 16 rows) and column slots (4, 2 or 1 up to 4, 8 and 16 rows, as
+// fit_slots leaves them); the VALU decode kernel runs one wave per run.
+static int group_of(const Geo &g, int rows, bool append = false) {
+  if (append) return 1;
+  if (rows <= 4 && g_decode_kernel.load() == kDecodeValu && select_valu(g)) return 1;
+  const int req = rows <= 4 ? 4 : rows <= 8 ? 2 : 1;
+  return run_waves(rows > 16 ? 2 : 1, fit_slots(g.bits, g.dp, g.bits == 16 ? 32 : g.group, req), append);
+}
 
-int attention_group(int rows) { return group_of(rows); }
+int attention_group(const Geo &g, int rows, bool append) { return group_of(g, rows, append); }
 
 bool append_fusable(const Geo &g, int rows) { return select_kernel(g, rows, true) != nullptr; }
 
@@ -1891,10 +1886,10 @@ int attention_waves(const Geo &g, int rows) {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64 * group_of(rows), 0) !=
-      hipSuccess)
+  const int gw = group_of(g, rows);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, 64 * gw, 0) != hipSuccess)
     return -1;
-  return max(1, cus * per_cu) * group_of(rows);  // resident waves (runs of group_of(rows))
+  return max(1, cus * per_cu) * gw;  // resident waves (runs of gw waves)
 }
 
 // The split charges each segment `lead` tiles ahead of its own, the cost of
@@ -1909,13 +1904,13 @@ int attention_waves(const Geo &g, int rows) {
 // the new token before its first tiles (C2: 67.8 us against 69.0 at 8).
 // A run of a grouped kernel (GW waves) moves GW tiles in a wave's tile time,
 // so its lead counts GW times as many tiles.
-int attention_lead(const Geo &, int rows, bool append) { return append ? 16 : 8 * group_of(rows); }
+int attention_lead(const Geo &g, int rows, bool append) { return append ? 16 : 8 * group_of(g, rows, append); }
 
 hipError_t launch_attention(hipStream_t stream, const AttnArgs &a) {
   const AttnKernel k = select_kernel(a.g, a.rows, a.new_k != nullptr);
   if (!k) return hipErrorInvalidValue;
   if (a.waves <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64 * group_of(a.rows)), 0, stream, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)a.waves), dim3(64 * group_of(a.g, a.rows, a.new_k != nullptr)), 0, stream, a);
   return hipGetLastError();
 }
 

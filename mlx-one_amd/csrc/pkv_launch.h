@@ -141,9 +141,10 @@ hipError_t launch_prefill(hipStream_t stream, const AttnArgs &a);
 // Resident waves of the attention kernel for this layout and row count on the
 // current device (CUs x workgroups per CU); <0 on error.
 int attention_waves(const Geo &g, int rows);
-// Waves per run of the split for `rows` query rows per KV head: a launch of W
-// waves has max(1, W / attention_group(rows)) runs, each with its partials.
-int attention_group(int rows);
+// Waves per run of the split for `rows` query rows per KV head (`append`: the
+// fused single-token form): a launch of W waves has
+// max(1, W / attention_group(rows, append)) runs, each with its partials.
+int attention_group(const Geo &g, int rows, bool append);
 // Lead tiles the decode split charges per segment for `rows` query rows per KV
 // head (more for a launch that fuses the single-token append).
 int attention_lead(const Geo &g, int rows, bool append);

@@ -149,7 +149,12 @@ def _fused_against_separate(overrides, waves):
     want = oracle_attention(fmt, inst, inst.positions, np.ones(w.batch, np.int32), scale)
     assert_attention_close(want_out.float().cpu().numpy(), want)
     assert_attention_close(got_out.float().cpu().numpy(), want)
-    # one wave: the same pieces in both forms, the same arithmetic
+    # one wave: the same pieces in both forms.  The fused form runs one wave
+    # per run; the separate attention of a two-column-slot shape runs each run
+    # on a group of four waves that meet by log-sum-exp, so its sums run in
+    # another order (and its P' operands, rounded to f16, see other running
+    # maxima): a bf16 step of the element plus 2^-9 of the row's largest
+    # element apart at most (single-wave shapes: equal).
     pool_c, _, _ = _context_pool(fmt, inst)
     ops.append_quantize(fmt, pool_c, k_new, v_new, table, lens - 1)
     one_a = ops.paged_attention(fmt, pool_c, q, table, lens, scale=scale, waves=1)
@@ -158,7 +163,10 @@ def _fused_against_separate(overrides, waves):
                                        waves=1)
     torch.cuda.synchronize()
     assert torch.equal(pool_c, pool_d), "pages differ (one wave)"
-    assert torch.equal(one_a, one_b), "outputs differ (one wave)"
+    a32, b32 = one_a.float(), one_b.float()
+    big = torch.maximum(a32.abs(), b32.abs())
+    bound = big * 2.0 ** -7 + big.amax(dim=-1, keepdim=True) * 2.0 ** -9
+    assert bool(((a32 - b32).abs() <= bound).all()), "outputs differ (one wave)"
 
 
 def test_fused_step_c2_full_size_against_the_oracle():
