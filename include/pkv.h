@@ -96,8 +96,10 @@ int pkv_append_quantize(void *stream, const pkv_layout *layout, void *pool, int6
  * (num_queries x num_heads / num_kv_heads; 16 at head_dim > 128): the
  * reference splits each sequence into fixed token partitions; here the
  * 16-token tiles of all (sequence, KV head) pairs are shared out as equal runs
- * over `waves` waves, and a pair whose tiles span several runs is merged by
- * log-sum-exp (:191-204) in a second kernel on the same stream.  Wider query
+ * over `waves` waves (for 5-8 and 17-32 rows per KV head, one run per four
+ * waves, which share its tiles and combine in LDS), and a pair whose tiles
+ * span several runs is merged by log-sum-exp (:191-204) in a second kernel on
+ * the same stream.  Wider query
  * blocks (up to 2^24 rows per KV head) run on an MFMA prefill kernel, 256
  * rows per workgroup (128 at head_dim > 128), that needs no workspace.
  * Mixed batches (the reference pads decode and prefill rows into one call,
