@@ -656,3 +656,49 @@ def test_attention_random_shapes_match_oracle(case):
     torch.cuda.synchronize()
     want = oracle_attention(fmt, inst, inst.positions, widths, scale)
     assert_attention_close(out.float().cpu().numpy(), want)
+
+
+# Grouped runs (5-8 and 17-32 rows per KV head: four waves per run, iterations
+# dealt round robin, states combined in LDS at each piece's end): pieces with
+# fewer iterations than the group (sequences of 1-40 tokens, many runs), one
+# run for everything (waves <= 4), runs ending inside a lead, and long pieces
+# next to short ones, at 4/8 bits and on bf16 pages.
+_GROUPED = [
+    dict(bits=8, head_dim=128, group_size=64, page_tokens=16, kv_heads=8, heads=64, num_queries=1,
+         batch=9, lengths=(1, 2, 3, 17, 33, 40, 5, 16, 31), waves=4000),
+    dict(bits=4, head_dim=128, group_size=64, page_tokens=32, kv_heads=4, heads=32, num_queries=1,
+         batch=3, lengths=(4096, 7, 1500), waves=3),
+    dict(bits=8, head_dim=128, group_size=64, page_tokens=16, kv_heads=8, heads=32, num_queries=5,
+         batch=6, lengths=(300, 1, 2, 900, 45, 64), waves=64),
+    dict(bits=8, head_dim=64, group_size=32, page_tokens=64, kv_heads=2, heads=16, num_queries=4,
+         batch=4, lengths=(1, 130, 2049, 16), waves=1),
+    dict(bits=4, head_dim=128, group_size=32, page_tokens=16, kv_heads=8, heads=32, num_queries=2,
+         batch=5, lengths=(3, 700, 64, 65, 1), waves=37),
+    dict(bits=16, head_dim=128, group_size=32, page_tokens=16, kv_heads=8, heads=32, num_queries=7,
+         batch=4, lengths=(20, 5, 333, 1024), waves=120),
+]
+
+
+@pytest.mark.parametrize("case", range(len(_GROUPED)))
+def test_grouped_runs_match_oracle(case):
+    from pkv import ops, workloads
+
+    case = dict(_GROUPED[case])
+    waves = case.pop("waves")
+    w = workloads.get("c2", shared_prefix_pages=0, outlier_fraction=0.0, length_range=(),
+                      append_tokens=case["num_queries"], seed=101 + len(case["lengths"]), **case)
+    inst = workloads.generate(w)
+    fmt = _fmt(w)
+    pool, table, lengths = fill_pages(fmt, inst, chunk=64)
+    widths = np.full(w.batch, w.num_queries, np.int32)
+    scale = scale_of(w.head_dim)
+    out = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
+                              scale=scale, q_pos=torch.from_numpy(inst.positions).cuda(),
+                              waves=waves)
+    again = ops.paged_attention(fmt, pool, to_torch(inst.queries, fmt.dtype), table, lengths,
+                                scale=scale, q_pos=torch.from_numpy(inst.positions).cuda(),
+                                waves=waves)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "grouped runs are not deterministic"
+    want = oracle_attention(fmt, inst, inst.positions, widths, scale)
+    assert_attention_close(out.float().cpu().numpy(), want)
