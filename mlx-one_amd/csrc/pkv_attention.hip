@@ -464,8 +464,43 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
   KT qv[RB][KB];
   KT qsl[SLOTS > 1 ? SLOTS : 1][KB];  // per slot: the lane's query operand in that slot's columns
   float qs[RB][NG];
+  // Grouped runs over quantized pages: the GW waves convert a piece's query
+  // operands together -- (row block, kb) pair i by wave i % GW -- and share
+  // them, with their f16 sums, through LDS (the same values and sums each
+  // wave would form); a row whose group sum overflows f16 takes the per-wave
+  // scaled conversion below.
+  constexpr bool QSHARE = QUANT && GW > 1;
+  constexpr int QPAIRS = RB * KB;
+  __shared__ u4 s_qop[QSHARE ? QPAIRS : 1][QSHARE ? 64 : 1];
+  __shared__ float s_qsum[QSHARE ? QPAIRS : 1][QSHARE ? 64 : 1];
   auto set_queries = [&](int pL, int pwidth, int t1, const u4 (&raw)[RB][KB], const int (&qp)[RB])
       __attribute__((always_inline)) {
+    if constexpr (QSHARE) {
+#pragma unroll
+      for (int i = 0; i < QPAIRS; ++i) {
+        if (i % GW != wk) continue;
+        const int rb = i / KB, kb = i % KB;
+        const int row = SLOTS > 1 ? rowc : rb * 16 + col;
+        const bool valid = row < a.rows;
+        const int d0 = 32 * kb + 8 * jj;
+        const u4 x = raw[rb][kb];
+        uint16_t e8[8] = {(uint16_t)(x.x & 0xFFFF), (uint16_t)(x.x >> 16), (uint16_t)(x.y & 0xFFFF),
+                          (uint16_t)(x.y >> 16), (uint16_t)(x.z & 0xFFFF), (uint16_t)(x.z >> 16),
+                          (uint16_t)(x.w & 0xFFFF), (uint16_t)(x.w >> 16)};
+        h8 v;
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const _Float16 hv = (_Float16)(bits_to_float(!valid || d0 + e >= g.dim ? (uint16_t)0 : e8[e],
+                                                       g.float_kind) * 1.0f);
+          v[e] = hv;
+          sum += (float)hv;
+        }
+        s_qop[i][lane] = __builtin_bit_cast(u4, v);
+        s_qsum[i][lane] = sum;
+      }
+      __syncthreads();
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const int row = SLOTS > 1 ? rowc : rb * 16 + col;
@@ -510,7 +545,15 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
         }
       }
       };
-      convert();
+      if constexpr (QSHARE) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          qv[rb][kb] = __builtin_bit_cast(KT, s_qop[rb * KB + kb][lane]);
+          qs[rb][(32 * kb) / G] += s_qsum[rb * KB + kb][lane];
+        }
+      } else {
+        convert();
+      }
       if constexpr (QUANT) {
         bool bad = false;
 #pragma unroll
