@@ -92,6 +92,31 @@ def test_workspace_size():
     assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1 << 23, 10) < 0
 
 
+def _parts(runs, rows, dp=128):
+    slots = 2 * runs
+    return -(-(slots * rows * 2 * 4) // 256) * 256 + slots * rows * dp * 4
+
+
+def test_workspace_size_of_grouped_runs():
+    """17-32 rows per KV head (two row blocks) and 5-8 (two column slots) run
+    each run of the split on four waves: a launch of W waves has W / 4 runs,
+    two partial slots each.  A shape whose fused single-token form runs one
+    wave per run (quantized pages, at most 8 rows) is sized for that form."""
+    lib = nat.load()
+    # 20 rows (5 queries at GQA 4): 100 waves = 25 runs
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 5, 100) == _parts(25, 20)
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 5, 3) == _parts(1, 20)  # at least one
+    # bf16 pages, 28 rows: grouped, no fused form
+    bf = _layout(bits=16, group_size=32)
+    assert lib.pkv_attention_workspace_bytes(bf, 32, 7, 100) == _parts(25, 28)
+    # 8 rows (GQA 8): grouped when separate, one wave per run when fused
+    assert lib.pkv_attention_workspace_bytes(_layout(), 64, 1, 100) == _parts(100, 8)
+    # ... and on bf16 pages (no fused form): grouped
+    assert lib.pkv_attention_workspace_bytes(bf, 64, 1, 100) == _parts(25, 8)
+    # 4 rows: one wave per run
+    assert lib.pkv_attention_workspace_bytes(_layout(), 32, 1, 100) == _parts(100, 4)
+
+
 def _attention(lib, layout, **kw):
     args = dict(stream=None, pool=FAKE, num_pages=10, q=FAKE, batch=2, heads=32, nq=1, table=FAKE,
                 max_pages=4, lens=FAKE, q_pos=None, widths=None, scale=0.1, waves=3,
