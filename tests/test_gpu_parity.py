@@ -542,13 +542,16 @@ def test_prefill_ragged_widths(positions_given):
     assert np.all(got[1, :, 17:] == 0) and np.all(got[2, :, 1:] == 0)
 
 
-def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays():
+@pytest.mark.parametrize("shape", [dict(), dict(num_queries=5, append_tokens=5), dict(heads=64)],
+                         ids=["rows4", "rows20_grouped", "rows8_grouped"])
+def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays(shape):
     """Split segments merged by log-sum-exp in a fixed piece order: back-to-back
     calls on one workspace, and replays of a captured graph (attention + merge
-    kernels, eager work between replays), each give the eager result bit for bit."""
+    kernels, eager work between replays), each give the eager result bit for bit
+    -- also for the grouped runs (LDS combine, barriers) of 8 and 20 rows."""
     from pkv import ops, workloads
 
-    w = workloads.get("c2", batch=6, length_range=(300, 2000))
+    w = workloads.get("c2", batch=6, length_range=(300, 2000), **shape)
     inst = workloads.generate(w)
     fmt = _fmt(w)
     pool, table, lengths = fill_pages(fmt, inst, chunk=128)
@@ -560,7 +563,8 @@ def test_split_segment_merge_is_deterministic_across_calls_and_graph_replays():
     second = ops.paged_attention(fmt, pool, q, table, lengths, scale=scale, q_pos=q_pos,
                                  waves=waves)
     torch.cuda.synchronize()
-    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, 1, np.int32), scale)
+    want = oracle_attention(fmt, inst, inst.positions, np.full(w.batch, w.num_queries, np.int32),
+                            scale)
     assert_attention_close(first.float().cpu().numpy(), want)
     assert torch.equal(first, second)
 
