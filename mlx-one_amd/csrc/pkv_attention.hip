@@ -1148,6 +1148,19 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           }
         }
       }
+      if constexpr (DEQ) {
+        static_assert(SLOTS == 1, "dequantized V rows take one column slot");
+        if (tail_it) {
+          // the lane's tokens past the piece's end (stale page bytes): scale
+          // and bias 0, so they dequantize to exact zeros (one select per
+          // word here rather than a branch per column block below)
+          const int tb = t0 + it * PKV_TILE + 4 * jj;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) vm[r * NG + gi] = tb + r < t1 ? vm[r * NG + gi] : 0u;
+        }
+      }
       // O^T += V^T . P'^T for each tile
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
@@ -1166,7 +1179,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
             VT vop;
             if constexpr (DEQ) {
               // the lane's four tokens 4jj..4jj+3 of column 16n + col,
-              // dequantized; tokens past the piece's end (stale metadata) zero
+              // dequantized (tokens past the piece's end: zero metadata)
               const int gi = (16 * n) / G;
               h4 sc, bi;
 #pragma unroll
@@ -1176,13 +1189,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
                 bi[r] = sb.y;
               }
               const h4 c = Conv<BITS>::template vop<C::LW>(vw[j], n);
-              u2 x = __builtin_bit_cast(u2, __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi));
-              if (tail_it) {
-                const int tb = t0 + (it * SLOTS + j) * PKV_TILE + 4 * jj;
-                x.x &= (tb < t1 ? 0x0000FFFFu : 0u) | (tb + 1 < t1 ? 0xFFFF0000u : 0u);
-                x.y &= (tb + 2 < t1 ? 0x0000FFFFu : 0u) | (tb + 3 < t1 ? 0xFFFF0000u : 0u);
-              }
-              vop = __builtin_bit_cast(VT, x);
+              vop = __builtin_bit_cast(VT, __builtin_elementwise_fma(c - (_Float16)1024.0f, sc, bi));
             } else if constexpr (QUANT) {
               vop = Conv<BITS>::template vop<C::LW>(vw[j], n);
             } else {
