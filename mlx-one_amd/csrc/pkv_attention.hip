@@ -961,15 +961,25 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
           }
         }
       }
-      // S^T for the iteration's tiles (slot j -> columns of slot j)
+      // S^T for the iteration's tiles (slot j -> columns of slot j).  Codes
+      // are finite whatever a register holds, and an absent tile's columns
+      // are masked by select (scores) or hold exact-zero P' operands, so
+      // quantized pages with several slots run every slot's products
+      // unguarded: straight-line code, no per-tile branches.
+      constexpr bool UNGUARDED = QUANT && SLOTS > 1;
+      // (unguarded chains start from zeros held in registers: an inline-zero
+      // accumulator would let the compiler place a chain's first product over
+      // part of its own operands)
+      f4 zacc = f4{0, 0, 0, 0};
+      if constexpr (UNGUARDED) asm volatile("" : "+v"(zacc));
       f4 acc[RB][NG];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int gi = 0; gi < NG; ++gi) acc[rb][gi] = f4{0, 0, 0, 0};
+        for (int gi = 0; gi < NG; ++gi) acc[rb][gi] = zacc;
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
-        if (cmask & (1 << j)) {
+        if (UNGUARDED || (cmask & (1 << j))) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             KT kop;
@@ -1164,7 +1174,7 @@ __attribute__((amdgpu_waves_per_eu(min_waves_per_simd(BITS, DP, G, RB, SLOTS))))
       // O^T += V^T . P'^T for each tile
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
-        if (cmask & (1 << j)) {
+        if (UNGUARDED || (cmask & (1 << j))) {
           VT bop[RB][NG], blo[SPLITP ? RB : 1];
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) {
