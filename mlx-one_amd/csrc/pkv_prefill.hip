@@ -703,23 +703,36 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
     const bool fast = oka && okb && ta + 1 < clear_tiles;
     float mx[RB];
     bool need = false;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+    // token (ta + i) * 16 + 4jj + r is visible to row block rb when
+    // i * 16 + r <= rel
+    auto mask = [&](int rb) __attribute__((always_inline)) {
+      const int rel = lim[rb] - ta * PKV_TILE - 4 * jj;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          v[rb][4 * i + r] = QUANT ? S[i][rb][r] : __builtin_fmaf(S[i][rb][r], rsc, -mb[rb]);
+        for (int r = 0; r < 4; ++r) {
+          const bool vis = (i ? okb : oka) && i * PKV_TILE + r <= rel;
+          v[rb][4 * i + r] = vis ? v[rb][4 * i + r] : -INFINITY;
+        }
+    };
+    if constexpr (QUANT) {  // the scores are S itself: one mask branch per step
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[rb][e] = S[e >> 2][rb][e & 3];
       if (!fast) {
-        // token (ta + i) * 16 + 4jj + r is visible when i * 16 + r <= rel
-        const int rel = lim[rb] - ta * PKV_TILE - 4 * jj;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) mask(rb);
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if constexpr (!QUANT) {  // (one branch per row block keeps fewer scores live)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const bool vis = (i ? okb : oka) && i * PKV_TILE + r <= rel;
-            v[rb][4 * i + r] = vis ? v[rb][4 * i + r] : -INFINITY;
-          }
+          for (int r = 0; r < 4; ++r) v[rb][4 * i + r] = __builtin_fmaf(S[i][rb][r], rsc, -mb[rb]);
+        if (!fast) mask(rb);
       }
       mx[rb] = max8(v[rb]);
       // before any token is seen every finite score sets the max
@@ -804,8 +817,8 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
   // issued before the first step's exponentials and the conversion halves
   // sit beside the PV MFMAs, so that the MFMA and VALU pipes overlap.  Both
   // run without branches: past the span the second step sees tiles flagged
-  // invalid (zeros, fully masked), and the last stage converts its own tile
-  // once more into the image nobody reads again.
+  // invalid (zeros, fully masked), and the last stage converts the absent
+  // tile past the span into the image nobody reads again.
   if (nstages > 0) {
     fetch(0);
     convert(0, true);
@@ -845,7 +858,7 @@ __global__ __launch_bounds__(64 * kMaxPrefillWaves) void prefill_kernel(const At
         convert(buf ^ 1, true);
       } else if (pr == 1) {
         convert(buf ^ 1, false);
-        if (s + 2 < nstages) fetch(s + 2);
+        fetch(s + 2);  // past the span: located as absent, no loads
       }
     }
     lds_barrier();
