@@ -389,7 +389,7 @@ def test_mixed_batch_routes_rows_per_sequence(case):
 _MIXED_GROUPS = {64: (32, 64), 128: (32, 64, 128), 256: (32, 64, 128)}
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", list(range(16)) + list(range(500, 530)))
 def test_mixed_batch_random(seed):
     """Seeded random mixed batches: 4-bit, int8 or bf16 pages, head_dim
     64/128/256, pages of 16-64 tokens, 1-8 query heads per KV head, and per
@@ -635,7 +635,8 @@ _RANDOM_REGRESSIONS = [
 # head runs on the prefill kernel)
 @pytest.mark.parametrize("case", _random_attention_cases(48, seed=2026) + _RANDOM_REGRESSIONS
                          + _random_attention_cases(32, seed=2027, dims=(64, 128, 256, 256),
-                                                   groups=(32, 64, 128), prefix="w"),
+                                                   groups=(32, 64, 128), prefix="w")
+                         + _random_attention_cases(60, seed=4001, prefix="x"),
                          ids=lambda c: f"r{c['index']}")
 def test_attention_random_shapes_match_oracle(case):
     """Random layouts (4/8-bit G32/G64 and bf16 pages, D 64-128, pages of
