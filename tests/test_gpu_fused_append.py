@@ -105,7 +105,7 @@ def test_fused_step_equals_append_then_attend(case):
 _GROUPS = {64: (32, 64), 100: (32,), 128: (32, 64, 128), 256: (32, 64, 128)}
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", list(range(24)) + list(range(100, 160)))
 def test_fused_step_random_shapes(seed):
     """Seeded random single-token steps over the shapes the fused launch
     serves (4 or 8 bits, head_dim 64/100/128/256 with their groups, pages of
@@ -153,8 +153,11 @@ def _fused_against_separate(overrides, waves):
     # per run; the separate attention of a two-column-slot shape runs each run
     # on a group of four waves that meet by log-sum-exp, so its sums run in
     # another order (and its P' operands, rounded to f16, see other running
-    # maxima): a bf16 step of the element plus 2^-9 of the row's largest
-    # element apart at most (single-wave shapes: equal).
+    # maxima): two bf16 steps of the element plus 2^-8 of the row's largest
+    # element apart at most (single-wave shapes: equal).  Seeded sweeps of
+    # 84 shapes put the largest gap at 4-bit pages, 8 rows per KV head: about
+    # 2^-7 of the row's largest element, the two forms' f32 sums rounding to
+    # bf16 values two steps apart; both forms meet the oracle's bar above.
     pool_c, _, _ = _context_pool(fmt, inst)
     ops.append_quantize(fmt, pool_c, k_new, v_new, table, lens - 1)
     one_a = ops.paged_attention(fmt, pool_c, q, table, lens, scale=scale, waves=1)
@@ -165,7 +168,7 @@ def _fused_against_separate(overrides, waves):
     assert torch.equal(pool_c, pool_d), "pages differ (one wave)"
     a32, b32 = one_a.float(), one_b.float()
     big = torch.maximum(a32.abs(), b32.abs())
-    bound = big * 2.0 ** -7 + big.amax(dim=-1, keepdim=True) * 2.0 ** -9
+    bound = big * 2.0 ** -6 + big.amax(dim=-1, keepdim=True) * 2.0 ** -8
     assert bool(((a32 - b32).abs() <= bound).all()), "outputs differ (one wave)"
 
 
